@@ -1,0 +1,179 @@
+/*
+ * wkv.h — C ABI of libwkv.so, the MI355X (gfx950) paged KV-cache decode path.
+ *
+ * The reference engine never touches KV memory itself: every append, block
+ * table read and paged attention happens inside the vLLM engine it drives
+ * (wavelet/inference/engine.py:818 builds it, :887 / :1045 / :1274 call
+ * llm.generate; wavelet/inference/server.py:323 / :1006 on the OpenAI
+ * backend). The entry points below replace the KV operations of that engine;
+ * each comment names the reference call site and the engine operation
+ * (vLLM's public custom-op name) it stands in for.
+ *
+ * Conventions
+ *   - All pointers are device pointers; sizes and strides are in elements.
+ *   - The library allocates nothing: caches, scales, block tables, outputs and
+ *     workspaces are owned by the caller (PyTorch in this repository).
+ *   - Every call is asynchronous on `stream` (a hipStream_t, NULL = default
+ *     stream) and never synchronises the host.
+ *   - Return value: 0 (WKV_OK) or a wkv_status_t. Arguments are validated on
+ *     the host before any launch; wkv_last_error() returns a thread-local
+ *     message for the last failure on the calling thread.
+ *   - Slot convention: slot = block_id * block_size + offset; slot -1 marks a
+ *     padded token that is skipped.
+ *
+ * Cache layout (one layer; x = 16 / element bytes, 8 for bf16, 16 for fp8):
+ *   k        [num_blocks, num_kv_heads, head_dim / x, block_size, x]
+ *   v        [num_blocks, num_kv_heads, head_dim, block_size]
+ *   k_scale, v_scale  [num_blocks, num_kv_heads] fp32, fp8 caches only
+ *   MLA latent [num_blocks, block_size, kv_lora_rank + rope_dim] bf16
+ * This is the paged-attention layout of the engine's ROCm backend: 16-byte
+ * runs of K along head_dim for one token, V transposed so one head_dim row of
+ * a block is contiguous.
+ */
+#ifndef WKV_H
+#define WKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WKV_ABI_VERSION 1
+
+typedef enum {
+  WKV_OK = 0,
+  WKV_ERR_INVALID = 1,     /* bad argument: shape, dtype, alignment, size */
+  WKV_ERR_UNSUPPORTED = 2, /* valid but not implemented (e.g. head_dim 96) */
+  WKV_ERR_LAUNCH = 3       /* the HIP runtime rejected a launch */
+} wkv_status_t;
+
+typedef enum { WKV_KV_BF16 = 0, WKV_KV_FP8_E4M3 = 1 } wkv_kv_dtype_t;
+
+/* One layer of a paged K/V cache. Replaces the per-layer KV tensors vLLM
+ * allocates from gpu_memory_utilization (engine.py:790-813; num_gpu_blocks x
+ * block_size is the capacity the reference reads back at
+ * wavelet/orchestrator/inference_metrics.py:125-133). */
+typedef struct {
+  void *k;
+  void *v;
+  float *k_scale; /* fp8 only, else NULL */
+  float *v_scale; /* fp8 only, else NULL */
+  int64_t num_blocks;
+  int32_t block_size;   /* multiple of 16 */
+  int32_t num_kv_heads;
+  int32_t head_dim;     /* 64 or 128 */
+  int32_t kv_dtype;     /* wkv_kv_dtype_t */
+} wkv_cache_t;
+
+/* One layer of an MLA latent cache (bf16). */
+typedef struct {
+  void *latent;
+  int64_t num_blocks;
+  int32_t block_size;   /* multiple of 16 */
+  int32_t kv_lora_rank; /* 512 */
+  int32_t rope_dim;     /* 64 */
+} wkv_mla_cache_t;
+
+/* ---- append -------------------------------------------------------------
+ * bf16 slot-mapped append: cache[slot[t]] = (key[t], value[t]) for slot >= 0.
+ * key/value: [num_tokens, num_kv_heads, head_dim] bf16, head_dim contiguous,
+ * strides multiples of 8 and base pointers 16-byte aligned.
+ * Replaces vLLM reshape_and_cache (reached through llm.generate,
+ * engine.py:887; HF analogue past_key_values.update,
+ * wavelet/kernels/patch.py:173-180). */
+int wkv_append(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
+               const void *value, int64_t value_stride_t, int64_t value_stride_h,
+               const int64_t *slot_mapping, int64_t num_tokens, void *stream);
+
+/* fp8-e4m3 append with one power-of-two fp32 scale per (block, head) for K
+ * and for V. Tokens are taken in runs (consecutive tokens of the call whose
+ * slots share a block); a run starting at offset 0 starts the block afresh,
+ * otherwise the scale may only grow and the block's earlier entries are
+ * re-encoded by the exact power-of-two ratio. Quantisation follows
+ * _fp8_roundtrip (wavelet/trainer/models/deepseek_v4/attention.py:41-50).
+ * A block may appear in at most one run per call.
+ * Replaces vLLM reshape_and_cache with kv_cache_dtype="fp8_e4m3" (enabled
+ * through inference.vllm.extra_args, wavelet/inference/server.py:1201-1212). */
+int wkv_append_fp8(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
+                   const void *value, int64_t value_stride_t, int64_t value_stride_h,
+                   const int64_t *slot_mapping, int64_t num_tokens, void *stream);
+
+/* MLA latent append: latent[slot[t]] = concat(kv_c[t], k_pe[t]).
+ * kv_c [T, kv_lora_rank], k_pe [T, rope_dim] bf16, row strides multiples of 8.
+ * Replaces vLLM concat_and_cache_mla (the MLA backend the reference patches
+ * at wavelet/inference/deepseek_v4.py:15-66). */
+int wkv_mla_append(const wkv_mla_cache_t *cache, const void *kv_c, int64_t kv_c_stride,
+                   const void *k_pe, int64_t k_pe_stride, const int64_t *slot_mapping,
+                   int64_t num_tokens, void *stream);
+
+/* ---- gather / block copy -------------------------------------------------
+ * Contiguous copy of each sequence's context:
+ *   out[cu_seq_lens[i] + t] = cache[block_table[i, t / bs], t % bs], t < seq_lens[i]
+ * out_k/out_v: [sum(seq_lens), num_kv_heads, head_dim]. With dequant = 0 the
+ * raw stored elements are copied (bf16, or fp8 codes); with dequant = 1 an fp8
+ * cache is written as bf16 code * scale (exact). block_table [batch, bt_stride]
+ * int32; seq_lens [batch] int32 <= max_blocks_per_seq * block_size;
+ * cu_seq_lens [batch] int64 exclusive prefix sums.
+ * Replaces vLLM gather_cache / gather_and_maybe_dequant_cache (prefix-cache
+ * reads inside llm.generate, engine.py:887; index semantics of
+ * attention.py:85-88 / :320-360). */
+int wkv_gather(const wkv_cache_t *cache, const int32_t *block_table, int64_t bt_stride,
+               int32_t max_blocks_per_seq, const int32_t *seq_lens, const int64_t *cu_seq_lens,
+               int32_t batch, void *out_k, void *out_v, int32_t dequant, void *stream);
+
+/* Copy whole blocks (K, V and fp8 scales): for i < n, block mapping[2i+1]
+ * becomes a copy of block mapping[2i]. Copy-on-write of a partially filled
+ * shared block when a GRPO group forks (n = num_generations sampling,
+ * engine.py:69-90). Replaces vLLM copy_blocks. */
+int wkv_copy_blocks(const wkv_cache_t *cache, const int64_t *block_mapping, int64_t n, void *stream);
+
+/* ---- paged decode attention ---------------------------------------------
+ * o[b, h] = softmax(q[b, h] . K_b^T * scale) . V_b over seq_lens[b] tokens read
+ * through block_table[b]; query head h reads KV head h / (num_q_heads /
+ * num_kv_heads). q: [batch, num_q_heads, head_dim] bf16 (head_dim contiguous,
+ * strides multiples of 8); out: [batch, num_q_heads, head_dim] bf16
+ * contiguous. max_seq_len must be >= every seq_lens[b]. partition_size
+ * (tokens, multiple of 16; 0 = library choice) splits long contexts into
+ * partitions; the last partition of each (sequence, KV head) to finish merges
+ * them by log-sum-exp in the same launch. When a context spans several
+ * partitions the call needs `workspace` (wkv_decode_workspace_size() bytes of
+ * scratch) and `tickets`: >= batch * num_kv_heads int32 counters that are zero
+ * on entry and that every call leaves zero again. Calls that share a tickets
+ * buffer must be ordered on one stream. A zero-length sequence gives zeros.
+ * Replaces vLLM paged_attention_v1/v2 and the ROCm paged-attention op (decode
+ * step of llm.generate, engine.py:887; semantics of attention.py:89-96 and the
+ * attention_interface call at wavelet/kernels/patch.py:182-196). */
+int64_t wkv_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim,
+                                  int32_t max_seq_len, int32_t partition_size);
+
+int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                         void *out, int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
+                         int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                         int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
+                         int64_t workspace_bytes, int32_t *tickets, int64_t num_tickets, void *stream);
+
+/* Weight-absorbed MLA decode over the latent cache:
+ *   s = (q_nope . c_kv + q_pe . k_pe) * scale; o = softmax(s) . c_kv
+ * q_nope [batch, num_heads, kv_lora_rank], q_pe [batch, num_heads, rope_dim]
+ * bf16 (last dim contiguous); out [batch, num_heads, kv_lora_rank] bf16.
+ * Replaces the vLLM MLA decode backend (FlashMLA, named at
+ * wavelet/inference/deepseek_v4.py:17, :64-66). */
+int64_t wkv_mla_workspace_size(int32_t batch, int32_t num_heads, int32_t kv_lora_rank,
+                               int32_t max_seq_len, int32_t partition_size);
+
+int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t qn_stride_b,
+                         int64_t qn_stride_h, const void *q_pe, int64_t qp_stride_b, int64_t qp_stride_h,
+                         void *out, int32_t num_heads, const int32_t *block_table, int64_t bt_stride,
+                         int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                         int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
+                         int64_t workspace_bytes, void *stream);
+
+/* ---- misc ---------------------------------------------------------------- */
+const char *wkv_last_error(void);
+int wkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WKV_H */

@@ -1,0 +1,193 @@
+"""GPU parity of paged decode attention against the float64 oracle.
+
+Tolerance (bf16 output): max |got - ref| <= 2e-2 and relative L2 <= 1e-2
+(kvcase.ATOL / kvcase.RTOL). Every slot a sequence does not own -- the tail of
+its last block and every unowned block -- holds NaN, so any read of a masked
+slot would show up as a non-finite output.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kvcase import ATOL, bits_of, check_attention, slots_for, to_dev_bits
+from oracle import fp8, paged
+from wavelet_amd import MLALatentCache, PagedKVCache, paged_decode_gqa, paged_decode_mla, synth
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+NAN16 = np.uint16(0x7FC0)
+
+
+def _owned_mask(w) -> np.ndarray:
+    """[NB, BS] True where some sequence's context covers the slot."""
+    own = np.zeros((w.num_blocks, w.block_size), bool)
+    for i in range(w.batch):
+        pos = np.arange(int(w.context_lens[i]))
+        own[w.block_tables[i][pos // w.block_size], pos % w.block_size] = True
+    return own
+
+
+def _bf16_caches(w, tag, std=1.0):
+    """Logical [NB, BS, H, D] bf16 bit caches, NaN outside every context."""
+    shape = (w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+    k = synth.normal_bf16(synth.stream_key(w.name, tag, "k"), shape, std=std)
+    v = synth.normal_bf16(synth.stream_key(w.name, tag, "v"), shape, std=std)
+    own = _owned_mask(w)
+    k[~own] = NAN16
+    v[~own] = NAN16
+    return k, v
+
+
+def _to_physical(k_log: np.ndarray, v_log: np.ndarray):
+    nb, bs, h, d = k_log.shape
+    x = 16 // k_log.dtype.itemsize
+    kp = np.ascontiguousarray(k_log.reshape(nb, bs, h, d // x, x).transpose(0, 2, 3, 1, 4))
+    vp = np.ascontiguousarray(v_log.transpose(0, 2, 3, 1))
+    return kp, vp
+
+
+def _run_gqa(w, cuda, k_log, v_log, q_bits, *, partition_size=0, max_seq_len=None):
+    cache = PagedKVCache(w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim, device=cuda)
+    kp, vp = _to_physical(k_log, v_log)
+    cache.k.copy_(to_dev_bits(kp, BF16, cuda))
+    cache.v.copy_(to_dev_bits(vp, BF16, cuda))
+    out = paged_decode_gqa(
+        to_dev_bits(q_bits, BF16, cuda), cache, torch.from_numpy(w.block_tables).to(cuda),
+        torch.from_numpy(w.context_lens).to(cuda), w.scale, partition_size=partition_size,
+        max_seq_len=max_seq_len,
+    )
+    return paged.bf16_to_f32(bits_of(out))
+
+
+def _gqa_case(w, cuda, tag="a", partition_size=0, q_std=1.0, kv_std=1.0):
+    k, v = _bf16_caches(w, tag, std=kv_std)
+    q = synth.normal_bf16(synth.stream_key(w.name, tag, "q"), (w.batch, w.num_q_heads, w.head_dim), std=q_std)
+    got = _run_gqa(w, cuda, k, v, q, partition_size=partition_size)
+    kf, vf = paged.bf16_to_f32(k), paged.bf16_to_f32(v)
+    qf = paged.bf16_to_f32(q)
+    ref = paged.decode_gqa(qf, kf, vf, w.block_tables, w.context_lens, w.scale)
+    ref_bf16 = paged.decode_gqa(qf, kf, vf, w.block_tables, w.context_lens, w.scale, p_bf16=True)
+    a, r = check_attention(got, ref, f"{w.name} P={partition_size}")
+    ra, rr = paged.max_abs_and_rel(paged.bf16_to_f32(paged.f32_to_bf16(ref_bf16.astype(np.float32))), ref)
+    print(f"{w.name} P={partition_size}: gpu err abs {a:.2e} rel {r:.2e} | reference bf16 path abs {ra:.2e} rel {rr:.2e}")
+
+
+def test_decode_qwen25_05b_shape(cuda):
+    """14 q / 2 kv heads, d=64, block 16, batch 128, contexts U{256..2048}; Q/K/V ~ N(0,1)/8."""
+    w = synth.qwen25_05b_workload()
+    _gqa_case(w, cuda, q_std=1 / 8, kv_std=1 / 8)
+
+
+def test_decode_qwen3_4b_shape_fixed_4096(cuda):
+    """32 q / 8 kv heads, d=128, block 16, context 4096 (batch reduced to 8 for the oracle)."""
+    w = synth.qwen3_4b_workload(batch=8)
+    _gqa_case(w, cuda)
+
+
+def test_decode_qwen3_4b_shape_variable_lengths(cuda):
+    w = synth.qwen3_4b_workload(batch=6, context=None)
+    for p in (0, 512):
+        _gqa_case(w, cuda, partition_size=p)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (28, 4, 128), (16, 1, 128), (8, 8, 64)])
+def test_decode_edge_lengths_and_partitions(cuda, hq, hkv, d):
+    lens = np.array([0, 1, 2, 15, 16, 17, 63, 255, 256, 257, 700, 1024])
+    w = synth.make_decode_workload(f"edge{hq}x{hkv}x{d}", batch=len(lens), num_kv_heads=hkv, num_q_heads=hq,
+                                   head_dim=d, block_size=16, context_lens=lens)
+    for p in (16, 64, 256, 0):
+        _gqa_case(w, cuda, tag=f"p{p}", partition_size=p)
+
+
+def test_decode_block_size_64(cuda):
+    lens = np.array([1, 64, 65, 500, 2048])
+    w = synth.make_decode_workload("bs64", batch=len(lens), num_kv_heads=4, num_q_heads=16, head_dim=128,
+                                   block_size=64, context_lens=lens)
+    _gqa_case(w, cuda, partition_size=128)
+
+
+def test_decode_reference_ignore_slot_known_answer(cuda):
+    """The reference's sigmoid(0.625)*[2,-1] answer with NaN in every never-read slot."""
+    from test_oracle import ignore_slot_case
+
+    kc, vc, q, bt, lens, scale, expected = ignore_slot_case()
+    w = synth.DecodeWorkload("ignore", num_blocks=2, block_size=16, num_kv_heads=1, num_q_heads=1, head_dim=64,
+                             context_lens=lens.astype(np.int32), block_tables=bt, scale=scale)
+    got = _run_gqa(w, cuda, paged.f32_to_bf16(kc), paged.f32_to_bf16(vc), paged.f32_to_bf16(q))
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got, expected, atol=1e-2, rtol=0)
+
+
+def test_decode_fp8_rollout_groups(cuda):
+    """Qwen2.5-7B shape groups (28 q / 4 kv, d=128), fp8 KV: 4 groups x 8 sharing a 1024-token prompt.
+
+    The cache is filled through the fp8 append path (prompt once per group in
+    whole-block runs, then each member's private tokens, then this step's
+    token) and checked bit-exact; attention reads the shared prompt blocks
+    from every member's block table.
+    """
+    w = synth.qwen25_7b_group_workload(num_groups=4)
+    H, D, BS, NB = w.num_kv_heads, w.head_dim, w.block_size, w.num_blocks
+    kc, vc = paged.empty_cache(NB, BS, H, D, dtype=np.uint8)
+    ks = np.zeros((NB, H), np.float32)
+    vs = np.zeros((NB, H), np.float32)
+    cache = PagedKVCache(NB, BS, H, D, kv_dtype="fp8_e4m3", device=cuda)
+
+    ctx = w.context_lens.astype(np.int64)
+    lo = np.where(np.arange(w.batch) % w.group_size == 0, 0, w.prefix_len)  # prompt written by member 0 only
+    steps = [("fill", slots_for(w, lo, ctx - 1)), ("new", w.new_token_slots())]
+    for name, sl in steps:
+        kb = synth.normal_bf16(synth.stream_key(w.name, name, "k"), (len(sl), H, D))
+        vb = synth.normal_bf16(synth.stream_key(w.name, name, "v"), (len(sl), H, D))
+        paged.append_fp8(kc, vc, ks, vs, kb, vb, sl)
+        cache.append(to_dev_bits(kb, BF16, cuda), to_dev_bits(vb, BF16, cuda), torch.from_numpy(sl).to(cuda))
+    assert np.array_equal(bits_of(cache.k), kc) and np.array_equal(bits_of(cache.v), vc)
+    np.testing.assert_array_equal(cache.k_scale.cpu().numpy(), ks)
+    np.testing.assert_array_equal(cache.v_scale.cpu().numpy(), vs)
+
+    q = synth.normal_bf16(synth.stream_key(w.name, "q"), (w.batch, w.num_q_heads, D))
+    out = paged_decode_gqa(to_dev_bits(q, BF16, cuda), cache, torch.from_numpy(w.block_tables).to(cuda),
+                           torch.from_numpy(w.context_lens).to(cuda), w.scale)
+    got = paged.bf16_to_f32(bits_of(out))
+    k_log = paged.k_logical(kc).reshape(NB, BS, H, D)
+    v_log = paged.v_logical(vc)
+    kf = fp8.dequantize(k_log, ks[:, None, :, None])
+    vf = fp8.dequantize(v_log, vs[:, None, :, None])
+    ref = paged.decode_gqa(paged.bf16_to_f32(q), kf, vf, w.block_tables, w.context_lens, w.scale)
+    a, r = check_attention(got, ref, "fp8 groups")
+    print(f"fp8 groups: err abs {a:.2e} rel {r:.2e}")
+
+
+def _mla_case(cuda, lens, heads=128, bs=64, partition_size=0, tag="m"):
+    R, P = 512, 64
+    w = synth.make_decode_workload(f"mla{tag}", batch=len(lens), num_kv_heads=1, num_q_heads=heads,
+                                   head_dim=R + P, block_size=bs, context_lens=np.asarray(lens),
+                                   scale=1 / math.sqrt(192.0))
+    own = _owned_mask(w)
+    lat = synth.normal_bf16(synth.stream_key(w.name, "lat"), (w.num_blocks, bs, R + P))
+    lat[~own] = NAN16
+    q = synth.normal_bf16(synth.stream_key(w.name, "q"), (w.batch, heads, R + P))
+    cache = MLALatentCache(w.num_blocks, bs, R, P, device=cuda)
+    cache.latent.copy_(to_dev_bits(lat, BF16, cuda))
+    dq = to_dev_bits(q, BF16, cuda)
+    out = paged_decode_mla(dq[:, :, :R], dq[:, :, R:], cache, torch.from_numpy(w.block_tables).to(cuda),
+                           torch.from_numpy(w.context_lens).to(cuda), w.scale, partition_size=partition_size)
+    got = paged.bf16_to_f32(bits_of(out))
+    ref = paged.decode_mla(paged.bf16_to_f32(q), paged.bf16_to_f32(lat), w.block_tables, w.context_lens, w.scale)
+    a, r = check_attention(got, ref, f"mla {tag}")
+    print(f"mla {tag}: err abs {a:.2e} rel {r:.2e}")
+
+
+def test_decode_mla_deepseek_v3_shape(cuda):
+    """128 heads over a 512+64 latent, block 64, context 4096 (batch reduced to 4 for the oracle)."""
+    _mla_case(cuda, [4096, 4096, 4096, 4096], tag="dsv3")
+
+
+@pytest.mark.parametrize("heads", [16, 128])
+def test_decode_mla_edge_lengths(cuda, heads):
+    for p in (64, 0):
+        _mla_case(cuda, [0, 1, 17, 64, 65, 300, 1000], heads=heads, partition_size=p, tag=f"edge{heads}p{p}")

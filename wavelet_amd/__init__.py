@@ -1,0 +1,21 @@
+"""MI355X-native paged KV-cache decode path (gfx950 HIP kernels behind a C ABI).
+
+Public surface (a drop-in for the KV path of the reference's inference engine):
+
+* ``PagedKVCache`` / ``MLALatentCache`` -- per-layer caches with ``append``,
+  ``gather`` and ``copy_blocks``;
+* ``paged_decode_gqa`` / ``paged_decode_mla`` -- one decode step of attention;
+* ``BlockManager`` -- host-side block allocation with ref-counted prefix
+  sharing for GRPO groups.
+"""
+
+from .attention import paged_decode_gqa, paged_decode_mla
+from .cache import MLALatentCache, PagedKVCache, validate_tables
+
+__all__ = [
+    "MLALatentCache",
+    "PagedKVCache",
+    "paged_decode_gqa",
+    "paged_decode_mla",
+    "validate_tables",
+]

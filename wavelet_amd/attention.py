@@ -1,0 +1,156 @@
+"""Paged decode attention over ``PagedKVCache`` / ``MLALatentCache``.
+
+The attention half of the engine's KV surface: for each decode step the
+reference's engine runs, per layer, ``softmax(q . K^T * scale) . V`` over each
+sequence's context read through its block table (inside ``llm.generate``,
+wavelet/inference/engine.py:887; semantics of ``_eager_sparse_attention``,
+wavelet/trainer/models/deepseek_v4/attention.py:81-96, and of the
+``attention_interface(..., scaling=self.scaling)`` call at
+wavelet/kernels/patch.py:182-196).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .cache import MLALatentCache, PagedKVCache, _require_cuda, _stream, check_tables
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_tickets: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _key(device: torch.device) -> tuple[int, int]:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return idx, torch.cuda.current_stream(device).cuda_stream
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-(device, stream) scratch for split-K partials, grown on demand and reused."""
+    key = _key(device)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def _ticket_buffer(device: torch.device, n: int) -> torch.Tensor:
+    """Per-(device, stream) int32 merge tickets: zeroed once, left zero by every call."""
+    key = _key(device)
+    t = _tickets.get(key)
+    if t is None or t.numel() < n:
+        t = torch.zeros(max(n, 4096), dtype=torch.int32, device=device)
+        _tickets[key] = t
+    return t
+
+
+def _query(q: torch.Tensor, name: str, shape: tuple[int, ...], device: torch.device) -> torch.Tensor:
+    _require_cuda(q, name, device)
+    if q.dtype != torch.bfloat16 or q.dim() != 3 or tuple(q.shape[1:]) != shape:
+        raise ValueError(f"{name} must be bfloat16 [B, {', '.join(map(str, shape))}] (got {q.dtype} {tuple(q.shape)})")
+    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    return q
+
+
+def _max_len(seq_lens: torch.Tensor, max_seq_len: int | None) -> int:
+    if max_seq_len is not None:
+        return int(max_seq_len)
+    return int(seq_lens.max().item()) if seq_lens.numel() else 0
+
+
+def paged_decode_gqa(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    scale: float,
+    *,
+    max_seq_len: int | None = None,
+    out: torch.Tensor | None = None,
+    partition_size: int = 0,
+) -> torch.Tensor:
+    """One decode step of GQA attention: ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` bf16.
+
+    Query head ``h`` reads KV head ``h // (Hq // Hkv)``. ``max_seq_len`` (a host
+    int, >= every ``seq_lens``) avoids a device sync when given.
+    """
+    if not isinstance(cache, PagedKVCache):
+        raise ValueError("cache must be a PagedKVCache")
+    dev = cache.device
+    block_table, seq_lens = check_tables(block_table, seq_lens, dev, cache.block_size)
+    batch = seq_lens.shape[0]
+    if q.dim() != 3 or q.shape[0] != batch:
+        raise ValueError(f"q must be [B={batch}, Hq, D]")
+    hq = q.shape[1]
+    q = _query(q, "q", (hq, cache.head_dim), dev)
+    if out is None:
+        out = torch.empty((batch, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, hq, cache.head_dim) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 [B, Hq, D] tensor")
+    if batch == 0:
+        return out
+    lib = _lib.load()
+    msl = _max_len(seq_lens, max_seq_len)
+    need = lib.wkv_decode_workspace_size(batch, hq, cache.head_dim, max(msl, 1), int(partition_size))
+    if need < 0:
+        raise ValueError("invalid decode geometry")
+    ws = _workspace(dev, need)
+    tk = _ticket_buffer(dev, batch * cache.num_kv_heads)
+    rc = lib.wkv_paged_decode_gqa(
+        ctypes.byref(cache.descriptor()), q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl,
+        float(scale), int(partition_size), ws.data_ptr(), ws.numel(), tk.data_ptr(), tk.numel(), _stream(dev),
+    )
+    _lib.check(rc, "paged_decode_gqa")
+    return out
+
+
+def paged_decode_mla(
+    q_nope: torch.Tensor,
+    q_pe: torch.Tensor,
+    cache: MLALatentCache,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    scale: float,
+    *,
+    max_seq_len: int | None = None,
+    out: torch.Tensor | None = None,
+    partition_size: int = 0,
+) -> torch.Tensor:
+    """Weight-absorbed MLA decode: ``q_nope [B, H, R]``, ``q_pe [B, H, P]`` -> ``[B, H, R]`` bf16."""
+    if not isinstance(cache, MLALatentCache):
+        raise ValueError("cache must be an MLALatentCache")
+    dev = cache.device
+    block_table, seq_lens = check_tables(block_table, seq_lens, dev, cache.block_size)
+    batch = seq_lens.shape[0]
+    if q_nope.dim() != 3 or q_nope.shape[0] != batch:
+        raise ValueError(f"q_nope must be [B={batch}, H, {cache.kv_lora_rank}]")
+    heads = q_nope.shape[1]
+    q_nope = _query(q_nope, "q_nope", (heads, cache.kv_lora_rank), dev)
+    q_pe = _query(q_pe, "q_pe", (heads, cache.rope_dim), dev)
+    if q_pe.shape[0] != batch:
+        raise ValueError("q_pe batch differs from q_nope")
+    if out is None:
+        out = torch.empty((batch, heads, cache.kv_lora_rank), dtype=torch.bfloat16, device=dev)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, heads, cache.kv_lora_rank) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 [B, H, R] tensor")
+    if batch == 0:
+        return out
+    lib = _lib.load()
+    msl = _max_len(seq_lens, max_seq_len)
+    need = lib.wkv_mla_workspace_size(batch, heads, cache.kv_lora_rank, max(msl, 1), int(partition_size))
+    if need < 0:
+        raise ValueError("invalid MLA decode geometry")
+    ws = _workspace(dev, need)
+    rc = lib.wkv_paged_decode_mla(
+        ctypes.byref(cache.descriptor()), q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1),
+        q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1), out.data_ptr(), heads,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl,
+        float(scale), int(partition_size), ws.data_ptr(), ws.numel(), _stream(dev),
+    )
+    _lib.check(rc, "paged_decode_mla")
+    return out

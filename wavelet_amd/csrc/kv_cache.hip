@@ -1,0 +1,393 @@
+// Slot-mapped append (bf16, fp8-e4m3 with per-(block, head) scales, MLA latent),
+// block-table gather and block copy for the paged KV cache.
+//
+// Cache layout (x = 16 / element bytes):
+//   K [NB, H, D/x, BS, x]   V [NB, H, D, BS]   scales [NB, H]   MLA [NB, BS, W]
+// These kernels move at most a few hundred KB per decode step; they are
+// launch-latency bound, so they favour one simple pass with 16-byte vector
+// accesses on the contiguous side over anything cleverer.
+#include "wkv_common.h"
+
+namespace wkv {
+
+// ---------------------------------------------------------------------------
+// bf16 append: one thread per (token, head, 8-element chunk).
+template <int D>
+__global__ __launch_bounds__(256) void append_bf16_kernel(uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+                                                          const uint16_t *__restrict__ key, int64_t kst,
+                                                          int64_t ksh, const uint16_t *__restrict__ val,
+                                                          int64_t vst, int64_t vsh,
+                                                          const int64_t *__restrict__ slots, int64_t T, int H,
+                                                          int BS, int64_t NB) {
+  constexpr int C = D / 8;
+  int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= T * H * C) return;
+  const int c = static_cast<int>(idx % C);
+  const int64_t th = idx / C;
+  const int h = static_cast<int>(th % H);
+  const int64_t t = th / H;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / BS;
+  const int off = static_cast<int>(slot % BS);
+  if (blk >= NB) return;  // out-of-range ids are never written (no fault)
+  const u32x4 kv = *reinterpret_cast<const u32x4 *>(key + t * kst + h * ksh + c * 8);
+  *reinterpret_cast<u32x4 *>(kc + (((blk * H + h) * C + c) * BS + off) * 8) = kv;
+  const u32x4 vv = *reinterpret_cast<const u32x4 *>(val + t * vst + h * vsh + c * 8);
+  uint16_t *vdst = vc + ((blk * H + h) * D + c * 8) * BS + off;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) vdst[j * BS] = static_cast<uint16_t>(vv[j >> 1] >> (16 * (j & 1)));
+}
+
+// ---------------------------------------------------------------------------
+// fp8 append: one wave per (token, head). Only the first token of a run (a
+// stretch of consecutive tokens whose slots share a block) does the work for
+// the whole run, so each (block, head) has exactly one writer per call.
+template <int D>
+__device__ __forceinline__ int64_t fp8_k_index(int64_t blk, int h, int H, int BS, int off, int d) {
+  return (((blk * H + h) * (D / 16) + (d >> 4)) * BS + off) * 16 + (d & 15);
+}
+template <int D>
+__device__ __forceinline__ int64_t fp8_v_index(int64_t blk, int h, int H, int BS, int off, int d) {
+  return ((blk * H + h) * D + d) * BS + off;
+}
+
+template <int D, bool IS_V>
+__device__ void fp8_append_one(uint8_t *__restrict__ cache, float *__restrict__ scales,
+                               const uint16_t *__restrict__ src, int64_t st, int64_t sh,
+                               const int64_t *__restrict__ slots, int64_t t, int r, int64_t blk, int first,
+                               int h, int H, int BS) {
+  const int lane = threadIdx.x;
+  float amax = 0.0f;
+  for (int e = lane; e < r * D; e += 64) {
+    const int tok = e / D, d = e % D;
+    amax = fmaxf(amax, fabsf(bf16_bits_to_f32(src[(t + tok) * st + h * sh + d])));
+  }
+  amax = wave_max(amax);
+  const float s_new = pow2_scale(amax);
+  float s = s_new;
+  if (first != 0) {
+    const float s_old = scales[blk * H + h];
+    s = (s_new > s_old) ? s_new : s_old;
+    if (s > s_old) {
+      const float ratio = s_old / s;  // exact power of two
+      for (int e = lane; e < first * D; e += 64) {
+        const int off = e / D, d = e % D;
+        const int64_t a = IS_V ? fp8_v_index<D>(blk, h, H, BS, off, d) : fp8_k_index<D>(blk, h, H, BS, off, d);
+        cache[a] = static_cast<uint8_t>(e4m3_encode(e4m3_decode(cache[a]) * ratio));
+      }
+    }
+  }
+  for (int e = lane; e < r * D; e += 64) {
+    const int tok = e / D, d = e % D;
+    const int off = static_cast<int>(slots[t + tok] % BS);
+    const float x = bf16_bits_to_f32(src[(t + tok) * st + h * sh + d]);
+    const int64_t a = IS_V ? fp8_v_index<D>(blk, h, H, BS, off, d) : fp8_k_index<D>(blk, h, H, BS, off, d);
+    cache[a] = static_cast<uint8_t>(e4m3_quantize(x, s));
+  }
+  if (lane == 0) scales[blk * H + h] = s;
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void append_fp8_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
+                                                        float *__restrict__ ks, float *__restrict__ vs,
+                                                        const uint16_t *__restrict__ key, int64_t kst,
+                                                        int64_t ksh, const uint16_t *__restrict__ val,
+                                                        int64_t vst, int64_t vsh,
+                                                        const int64_t *__restrict__ slots, int64_t T, int H,
+                                                        int BS, int64_t NB) {
+  const int64_t t = blockIdx.x;
+  const int h = blockIdx.y;
+  const int64_t slot = slots[t];
+  if (slot < 0) return;
+  const int64_t blk = slot / BS;
+  if (blk >= NB) return;
+  if (t > 0) {
+    const int64_t prev = slots[t - 1];
+    if (prev >= 0 && prev / BS == blk) return;  // not the first token of its run
+  }
+  int r = 1;
+  while (t + r < T) {
+    const int64_t nx = slots[t + r];
+    if (nx < 0 || nx / BS != blk) break;
+    ++r;
+  }
+  const int first = static_cast<int>(slot % BS);
+  fp8_append_one<D, false>(kc, ks, key, kst, ksh, slots, t, r, blk, first, h, H, BS);
+  fp8_append_one<D, true>(vc, vs, val, vst, vsh, slots, t, r, blk, first, h, H, BS);
+}
+
+// ---------------------------------------------------------------------------
+// Gather: one workgroup per (sequence, block index). Reads follow the
+// physical order (coalesced); writes are 16-byte pieces of the contiguous
+// [tokens, H, D] output.
+template <int D, bool FP8, bool DEQUANT>
+__global__ __launch_bounds__(256) void gather_kernel(const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc,
+                                                     const float *__restrict__ ks, const float *__restrict__ vs,
+                                                     const int32_t *__restrict__ bt, int64_t bt_stride, int Mb,
+                                                     const int32_t *__restrict__ seq_lens,
+                                                     const int64_t *__restrict__ cu, uint8_t *__restrict__ out_k,
+                                                     uint8_t *__restrict__ out_v, int H, int BS, int64_t NB) {
+  constexpr int ESZ = FP8 ? 1 : 2;        // stored element bytes
+  constexpr int OSZ = DEQUANT ? 2 : ESZ;  // output element bytes
+  constexpr int X = 16 / ESZ;             // elements per 16-byte K chunk
+  constexpr int C = D / X;
+  const int i = blockIdx.y, j = blockIdx.x;
+  int L = seq_lens[i];
+  L = L < Mb * BS ? L : Mb * BS;
+  if (L <= 0 || j * BS >= L) return;
+  const int64_t blk = bt[i * bt_stride + j];
+  if (blk < 0 || blk >= NB) return;
+  const int ntok = (L - j * BS) < BS ? (L - j * BS) : BS;
+  const int64_t tok0 = cu[i] + static_cast<int64_t>(j) * BS;
+
+  // K: work item = one 16-byte chunk (X elements of one token, one head).
+  for (int w = threadIdx.x; w < H * C * ntok; w += 256) {
+    const int o = w % ntok, hc = w / ntok, c = hc % C, h = hc / C;
+    const u32x4 raw = *reinterpret_cast<const u32x4 *>(kc + ((((blk * H + h) * C + c) * BS + o) * 16));
+    uint8_t *dst = out_k + (((tok0 + o) * H + h) * D + c * X) * OSZ;
+    if constexpr (!DEQUANT) {
+      *reinterpret_cast<u32x4 *>(dst) = raw;
+    } else {
+      const float s = ks[blk * H + h];
+      u32x4 lo, hi;
+#pragma unroll
+      for (int q = 0; q < 16; q += 2) {
+        const uint32_t b0 = (raw[q >> 2] >> (8 * (q & 3))) & 0xffu;
+        const uint32_t b1 = (raw[q >> 2] >> (8 * ((q & 3) + 1))) & 0xffu;
+        const uint32_t pk = f32_to_bf16_bits(e4m3_decode(b0) * s) | (f32_to_bf16_bits(e4m3_decode(b1) * s) << 16);
+        if (q < 8) lo[q >> 1] = pk; else hi[(q - 8) >> 1] = pk;
+      }
+      reinterpret_cast<u32x4 *>(dst)[0] = lo;
+      reinterpret_cast<u32x4 *>(dst)[1] = hi;
+    }
+  }
+  // V: work item = 8 consecutive d of one token and head (stride BS in the cache).
+  for (int w = threadIdx.x; w < H * (D / 8) * ntok; w += 256) {
+    const int o = w % ntok, hg = w / ntok, g = hg % (D / 8), h = hg / (D / 8);
+    const int64_t base = ((blk * H + h) * D + g * 8) * BS + o;
+    uint8_t *dst = out_v + (((tok0 + o) * H + h) * D + g * 8) * OSZ;
+    if constexpr (!FP8) {
+      const uint16_t *src = reinterpret_cast<const uint16_t *>(vc);
+      u32x4 pk;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        pk[q] = static_cast<uint32_t>(src[base + (2 * q) * BS]) | (static_cast<uint32_t>(src[base + (2 * q + 1) * BS]) << 16);
+      *reinterpret_cast<u32x4 *>(dst) = pk;
+    } else if constexpr (!DEQUANT) {
+      u32x2 pk;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) wv |= static_cast<uint32_t>(vc[base + (4 * q + b) * BS]) << (8 * b);
+        pk[q] = wv;
+      }
+      *reinterpret_cast<u32x2 *>(dst) = pk;
+    } else {
+      const float s = vs[blk * H + h];
+      u32x4 pk;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        pk[q] = f32_to_bf16_bits(e4m3_decode(vc[base + (2 * q) * BS]) * s) |
+                (f32_to_bf16_bits(e4m3_decode(vc[base + (2 * q + 1) * BS]) * s) << 16);
+      *reinterpret_cast<u32x4 *>(dst) = pk;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Whole-block copy (K, V, scales): one workgroup per (src, dst) pair.
+__global__ __launch_bounds__(256) void copy_blocks_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
+                                                          float *__restrict__ ks, float *__restrict__ vs,
+                                                          const int64_t *__restrict__ mapping, int64_t block_bytes,
+                                                          int H, int64_t NB) {
+  const int64_t src = mapping[2 * blockIdx.x], dst = mapping[2 * blockIdx.x + 1];
+  if (src < 0 || dst < 0 || src >= NB || dst >= NB) return;
+  const int64_t n16 = block_bytes / 16;
+  const u32x4 *ks4 = reinterpret_cast<const u32x4 *>(kc + src * block_bytes);
+  const u32x4 *vs4 = reinterpret_cast<const u32x4 *>(vc + src * block_bytes);
+  u32x4 *kd4 = reinterpret_cast<u32x4 *>(kc + dst * block_bytes);
+  u32x4 *vd4 = reinterpret_cast<u32x4 *>(vc + dst * block_bytes);
+  for (int64_t w = threadIdx.x; w < n16; w += 256) {
+    kd4[w] = ks4[w];
+    vd4[w] = vs4[w];
+  }
+  if (ks != nullptr && threadIdx.x < H) {
+    ks[dst * H + threadIdx.x] = ks[src * H + threadIdx.x];
+    vs[dst * H + threadIdx.x] = vs[src * H + threadIdx.x];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MLA latent append: one thread per (token, 8-element chunk of the W-wide row).
+__global__ __launch_bounds__(256) void mla_append_kernel(uint16_t *__restrict__ lat, const uint16_t *__restrict__ kvc,
+                                                         int64_t kvc_st, const uint16_t *__restrict__ kpe,
+                                                         int64_t kpe_st, const int64_t *__restrict__ slots,
+                                                         int64_t T, int R, int P, int BS, int64_t NB) {
+  const int W = R + P, C = W / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= T * C) return;
+  const int c = static_cast<int>(idx % C);
+  const int64_t t = idx / C;
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot / BS >= NB) return;
+  const uint16_t *src = (c * 8 < R) ? kvc + t * kvc_st + c * 8 : kpe + t * kpe_st + (c * 8 - R);
+  *reinterpret_cast<u32x4 *>(lat + slot * W + c * 8) = *reinterpret_cast<const u32x4 *>(src);
+}
+
+static int check_kv_input(const void *p, int64_t st_t, int64_t st_h, const char *name) {
+  WKV_CHECK_ARG(p != nullptr, "%s is NULL", name);
+  WKV_CHECK_ARG(aligned16(p), "%s must be 16-byte aligned", name);
+  WKV_CHECK_ARG(st_t % 8 == 0 && st_h % 8 == 0 && st_t >= 0 && st_h >= 0,
+                "%s strides must be non-negative multiples of 8 (got %lld, %lld)", name, (long long)st_t,
+                (long long)st_h);
+  return WKV_OK;
+}
+
+}  // namespace wkv
+
+using namespace wkv;
+
+extern "C" int wkv_append(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
+                          const void *value, int64_t value_stride_t, int64_t value_stride_h,
+                          const int64_t *slot_mapping, int64_t num_tokens, void *stream) {
+  int rc = check_cache(cache, WKV_KV_BF16);
+  if (rc) return rc;
+  WKV_CHECK_ARG(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return WKV_OK;
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  if ((rc = check_kv_input(key, key_stride_t, key_stride_h, "key"))) return rc;
+  if ((rc = check_kv_input(value, value_stride_t, value_stride_h, "value"))) return rc;
+  const int H = cache->num_kv_heads, D = cache->head_dim;
+  const int64_t work = num_tokens * H * (D / 8);
+  const dim3 grid(static_cast<unsigned>((work + 255) / 256));
+  auto s = static_cast<hipStream_t>(stream);
+  auto kc = static_cast<uint16_t *>(cache->k);
+  auto vc = static_cast<uint16_t *>(cache->v);
+  auto k = static_cast<const uint16_t *>(key);
+  auto v = static_cast<const uint16_t *>(value);
+  if (D == 128)
+    append_bf16_kernel<128><<<grid, 256, 0, s>>>(kc, vc, k, key_stride_t, key_stride_h, v, value_stride_t,
+                                                 value_stride_h, slot_mapping, num_tokens, H, cache->block_size,
+                                                 cache->num_blocks);
+  else
+    append_bf16_kernel<64><<<grid, 256, 0, s>>>(kc, vc, k, key_stride_t, key_stride_h, v, value_stride_t,
+                                                value_stride_h, slot_mapping, num_tokens, H, cache->block_size,
+                                                cache->num_blocks);
+  WKV_CHECK_LAUNCH("wkv_append");
+  return WKV_OK;
+}
+
+extern "C" int wkv_append_fp8(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                              int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                              int64_t value_stride_h, const int64_t *slot_mapping, int64_t num_tokens,
+                              void *stream) {
+  int rc = check_cache(cache, WKV_KV_FP8_E4M3);
+  if (rc) return rc;
+  WKV_CHECK_ARG(num_tokens >= 0 && num_tokens < (1ll << 31), "num_tokens out of range");
+  if (num_tokens == 0) return WKV_OK;
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  if ((rc = check_kv_input(key, key_stride_t, key_stride_h, "key"))) return rc;
+  if ((rc = check_kv_input(value, value_stride_t, value_stride_h, "value"))) return rc;
+  WKV_CHECK_ARG(cache->num_kv_heads <= 65535, "num_kv_heads too large");
+  const int H = cache->num_kv_heads, D = cache->head_dim;
+  const dim3 grid(static_cast<unsigned>(num_tokens), static_cast<unsigned>(H));
+  auto s = static_cast<hipStream_t>(stream);
+  auto kc = static_cast<uint8_t *>(cache->k);
+  auto vc = static_cast<uint8_t *>(cache->v);
+  auto k = static_cast<const uint16_t *>(key);
+  auto v = static_cast<const uint16_t *>(value);
+  if (D == 128)
+    append_fp8_kernel<128><<<grid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
+                                               key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
+                                               num_tokens, H, cache->block_size, cache->num_blocks);
+  else
+    append_fp8_kernel<64><<<grid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
+                                              key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
+                                              num_tokens, H, cache->block_size, cache->num_blocks);
+  WKV_CHECK_LAUNCH("wkv_append_fp8");
+  return WKV_OK;
+}
+
+extern "C" int wkv_mla_append(const wkv_mla_cache_t *cache, const void *kv_c, int64_t kv_c_stride,
+                              const void *k_pe, int64_t k_pe_stride, const int64_t *slot_mapping,
+                              int64_t num_tokens, void *stream) {
+  WKV_CHECK_ARG(cache != nullptr && cache->latent != nullptr, "MLA cache is NULL");
+  WKV_CHECK_ARG(aligned16(cache->latent), "MLA latent cache must be 16-byte aligned");
+  WKV_CHECK_ARG(cache->num_blocks > 0 && cache->block_size > 0 && cache->block_size % 16 == 0,
+                "bad MLA cache geometry");
+  WKV_CHECK_ARG(cache->kv_lora_rank % 8 == 0 && cache->rope_dim % 8 == 0 && cache->kv_lora_rank > 0 &&
+                    cache->rope_dim >= 0,
+                "kv_lora_rank and rope_dim must be multiples of 8");
+  WKV_CHECK_ARG(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return WKV_OK;
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  int rc;
+  if ((rc = check_kv_input(kv_c, kv_c_stride, 0, "kv_c"))) return rc;
+  if (cache->rope_dim > 0 && (rc = check_kv_input(k_pe, k_pe_stride, 0, "k_pe"))) return rc;
+  const int C = (cache->kv_lora_rank + cache->rope_dim) / 8;
+  const dim3 grid(static_cast<unsigned>((num_tokens * C + 255) / 256));
+  mla_append_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<uint16_t *>(cache->latent), static_cast<const uint16_t *>(kv_c), kv_c_stride,
+      static_cast<const uint16_t *>(k_pe), k_pe_stride, slot_mapping, num_tokens, cache->kv_lora_rank,
+      cache->rope_dim, cache->block_size, cache->num_blocks);
+  WKV_CHECK_LAUNCH("wkv_mla_append");
+  return WKV_OK;
+}
+
+extern "C" int wkv_gather(const wkv_cache_t *cache, const int32_t *block_table, int64_t bt_stride,
+                          int32_t max_blocks_per_seq, const int32_t *seq_lens, const int64_t *cu_seq_lens,
+                          int32_t batch, void *out_k, void *out_v, int32_t dequant, void *stream) {
+  int rc = check_cache(cache, -1);
+  if (rc) return rc;
+  WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535]");
+  if (batch == 0 || max_blocks_per_seq == 0) return WKV_OK;
+  WKV_CHECK_ARG(max_blocks_per_seq > 0 && bt_stride >= max_blocks_per_seq, "bad block table geometry");
+  WKV_CHECK_ARG(block_table && seq_lens && cu_seq_lens, "block_table / seq_lens / cu_seq_lens is NULL");
+  WKV_CHECK_ARG(out_k && out_v && aligned16(out_k) && aligned16(out_v), "outputs must be non-NULL and 16-byte aligned");
+  WKV_CHECK_ARG(dequant == 0 || dequant == 1, "dequant must be 0 or 1");
+  const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
+  WKV_CHECK_ARG(!dequant || fp8, "dequant applies to fp8 caches only");
+  const dim3 grid(static_cast<unsigned>(max_blocks_per_seq), static_cast<unsigned>(batch));
+  auto s = static_cast<hipStream_t>(stream);
+  auto kc = static_cast<const uint8_t *>(cache->k);
+  auto vc = static_cast<const uint8_t *>(cache->v);
+  auto ok = static_cast<uint8_t *>(out_k);
+  auto ov = static_cast<uint8_t *>(out_v);
+  const int H = cache->num_kv_heads, BS = cache->block_size;
+  const int64_t NB = cache->num_blocks;
+#define WKV_GATHER(Dv, F8, DQ)                                                                               \
+  gather_kernel<Dv, F8, DQ><<<grid, 256, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, block_table, bt_stride, \
+                                                 max_blocks_per_seq, seq_lens, cu_seq_lens, ok, ov, H, BS, NB)
+  if (cache->head_dim == 128) {
+    if (!fp8) WKV_GATHER(128, false, false);
+    else if (!dequant) WKV_GATHER(128, true, false);
+    else WKV_GATHER(128, true, true);
+  } else {
+    if (!fp8) WKV_GATHER(64, false, false);
+    else if (!dequant) WKV_GATHER(64, true, false);
+    else WKV_GATHER(64, true, true);
+  }
+#undef WKV_GATHER
+  WKV_CHECK_LAUNCH("wkv_gather");
+  return WKV_OK;
+}
+
+extern "C" int wkv_copy_blocks(const wkv_cache_t *cache, const int64_t *block_mapping, int64_t n, void *stream) {
+  int rc = check_cache(cache, -1);
+  if (rc) return rc;
+  WKV_CHECK_ARG(n >= 0 && n < (1ll << 31), "n out of range");
+  if (n == 0) return WKV_OK;
+  WKV_CHECK_ARG(block_mapping != nullptr, "block_mapping is NULL");
+  const int esz = cache->kv_dtype == WKV_KV_FP8_E4M3 ? 1 : 2;
+  const int64_t block_bytes =
+      static_cast<int64_t>(cache->num_kv_heads) * cache->head_dim * cache->block_size * esz;
+  WKV_CHECK_ARG(cache->num_kv_heads <= 256, "copy_blocks supports at most 256 KV heads");
+  const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
+  copy_blocks_kernel<<<dim3(static_cast<unsigned>(n)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<uint8_t *>(cache->k), static_cast<uint8_t *>(cache->v), fp8 ? cache->k_scale : nullptr,
+      fp8 ? cache->v_scale : nullptr, block_mapping, block_bytes, cache->num_kv_heads, cache->num_blocks);
+  WKV_CHECK_LAUNCH("wkv_copy_blocks");
+  return WKV_OK;
+}

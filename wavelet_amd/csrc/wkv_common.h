@@ -1,0 +1,117 @@
+// Shared device helpers and host-side validation for libwkv (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/wkv.h"
+
+namespace wkv {
+
+// ---------------------------------------------------------------------------
+// Vector types matching the MFMA builtin operand types.
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float floatx2;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+// ---------------------------------------------------------------------------
+// Host-side error state (thread-local message, set before returning non-zero).
+void set_error(const char *fmt, ...);
+int fail(int code, const char *fmt, ...);
+
+#define WKV_CHECK_ARG(cond, ...)                      \
+  do {                                                \
+    if (!(cond)) return ::wkv::fail(WKV_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define WKV_CHECK_LAUNCH(what)                                                        \
+  do {                                                                                \
+    hipError_t e_ = hipGetLastError();                                                \
+    if (e_ != hipSuccess)                                                             \
+      return ::wkv::fail(WKV_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e_));     \
+  } while (0)
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Validates the parts of a cache descriptor every entry point relies on.
+// want_dtype: a wkv_kv_dtype_t the entry point requires, or -1 for either.
+int check_cache(const wkv_cache_t *c, int want_dtype);
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32 (bit level, RNE, NaN kept quiet) — matches torch's conversion.
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// ---------------------------------------------------------------------------
+// fp8 e4m3fn (OCP) encode, bit-identical to torch's fp32 -> float8_e4m3fn
+// cast: RNE, no saturation (a value rounding above 448 becomes 0x7F | sign),
+// NaN -> 0x7F | sign.
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+  uint32_t bits = __float_as_uint(x);
+  uint32_t sign = (bits >> 24) & 0x80u;
+  uint32_t a = bits & 0x7fffffffu;
+  if (a >= 0x43f00000u) return 0x7fu | sign;  // >= 480, inf, NaN
+  if (a < 0x3c800000u) {                      // < 2^-6: multiples of 2^-9
+    float q = rintf(__uint_as_float(a) * 512.0f);
+    return static_cast<uint32_t>(q) | sign;
+  }
+  uint32_t e = (a >> 23) - 127u + 7u;  // biased e4m3 exponent, 1..15
+  uint32_t mant = a & 0x7fffffu;
+  uint32_t r = mant >> 20;
+  uint32_t rem = mant & 0xfffffu;
+  r += (rem > 0x80000u) || (rem == 0x80000u && (r & 1u));
+  uint32_t code = (e << 3) + r;
+  if (code > 0x7eu) code = 0x7fu;
+  return code | sign;
+}
+
+__device__ __forceinline__ float e4m3_decode(uint32_t c) {
+  uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+  float mag;
+  if (e == 0)
+    mag = static_cast<float>(m) * 0.001953125f;  // 2^-9
+  else if (e == 15 && m == 7)
+    mag = __uint_as_float(0x7fc00000u);
+  else
+    mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (c & 0x80u) ? -mag : mag;
+}
+
+// Smallest power of two >= max(amax, 1e-10) / 448 (fp32 division), amax
+// clamped to FLT_MAX first; the exponent is read from the bits, no log2.
+__device__ __forceinline__ float pow2_scale(float amax) {
+  float a = fminf(fmaxf(amax, 1e-10f), 3.402823466e38f);
+  float r = a / 448.0f;
+  uint32_t u = __float_as_uint(r);
+  uint32_t e = u >> 23;            // r is normal: >= 2^-42
+  if ((u & 0x7fffffu) != 0) e += 1;  // not a power of two: round the exponent up
+  return __uint_as_float(e << 23);
+}
+
+// fp32 -> e4m3 after clamping to +-448 (NaN passes through to the NaN code).
+__device__ __forceinline__ uint32_t e4m3_quantize(float x, float scale) {
+  float v = x / scale;  // scale is a power of two: the quotient is exact
+  v = (v != v) ? v : fminf(fmaxf(v, -448.0f), 448.0f);
+  return e4m3_encode(v);
+}
+
+// ---------------------------------------------------------------------------
+// Wavefront helpers (wave64).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace wkv

@@ -1,0 +1,97 @@
+"""Pre-validated decode-step launch plans.
+
+A serving loop calls append + attention once per layer per decode step with
+buffers whose shapes never change between steps. ``DecodeStep`` validates
+those buffers once, resolves every pointer, stride and workspace, and then
+replays the C-ABI calls directly -- two ctypes calls per layer and no tensor
+inspection -- so host overhead stays far below the GPU time of a step.
+The tensors handed to it must stay alive (and keep their storage) for the
+plan's lifetime; refill them in place between steps.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .attention import _ticket_buffer, _workspace
+from .cache import PagedKVCache, check_tables
+
+
+@dataclass
+class _LayerCall:
+    append_fn: object
+    append_args: tuple
+    decode_args: tuple
+
+
+class DecodeStep:
+    """Append one token per sequence, then GQA decode attention, for every layer.
+
+    ``caches[l]`` is layer ``l``'s cache; ``q[l]`` ``[B, Hq, D]``, ``key[l]`` /
+    ``value[l]`` ``[T, Hkv, D]`` and ``out[l]`` ``[B, Hq, D]`` are the per-layer
+    step buffers; ``block_table`` / ``seq_lens`` / ``slot_mapping`` are shared by
+    all layers (as in a paged engine, one table per sequence).
+    """
+
+    def __init__(self, caches: list[PagedKVCache], q: list[torch.Tensor], key: list[torch.Tensor],
+                 value: list[torch.Tensor], out: list[torch.Tensor], block_table: torch.Tensor,
+                 seq_lens: torch.Tensor, slot_mapping: torch.Tensor, scale: float, max_seq_len: int,
+                 partition_size: int = 0) -> None:
+        if not caches:
+            raise ValueError("no layers")
+        dev = caches[0].device
+        c0 = caches[0]
+        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, c0.block_size)
+        if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+            raise ValueError("slot_mapping must be a contiguous int64 vector")
+        self.slot_mapping = slot_mapping
+        batch = self.seq_lens.shape[0]
+        lib = _lib.load()
+        hq = q[0].shape[1]
+        need = lib.wkv_decode_workspace_size(batch, hq, c0.head_dim, max_seq_len, int(partition_size))
+        if need < 0:
+            raise ValueError("invalid decode geometry")
+        self.workspace = _workspace(dev, need)
+        self.tickets = _ticket_buffer(dev, batch * c0.num_kv_heads)
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+        self.lib = lib
+        self.calls: list[_LayerCall] = []
+        for layer, cache in enumerate(caches):
+            qq, kk, vv, oo = q[layer], key[layer], value[layer], out[layer]
+            for name, t, shape in (("q", qq, (batch, hq, cache.head_dim)), ("out", oo, (batch, hq, cache.head_dim)),
+                                   ("key", kk, (slot_mapping.numel(), cache.num_kv_heads, cache.head_dim)),
+                                   ("value", vv, (slot_mapping.numel(), cache.num_kv_heads, cache.head_dim))):
+                if t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous() or t.device != dev:
+                    raise ValueError(f"layer {layer}: {name} must be a contiguous bfloat16 {shape} tensor on {dev}")
+            fn = lib.wkv_append_fp8 if cache.kv_dtype == "fp8_e4m3" else lib.wkv_append
+            desc = ctypes.byref(cache.descriptor())
+            append_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
+                           vv.stride(1), slot_mapping.data_ptr(), slot_mapping.numel(), self.stream)
+            decode_args = (desc, qq.data_ptr(), qq.stride(0), qq.stride(1), oo.data_ptr(), hq,
+                           self.block_table.data_ptr(), self.block_table.stride(0), self.block_table.shape[1],
+                           self.seq_lens.data_ptr(), batch, int(max_seq_len), ctypes.c_float(scale),
+                           int(partition_size), self.workspace.data_ptr(), self.workspace.numel(),
+                           self.tickets.data_ptr(), self.tickets.numel(), self.stream)
+            self.calls.append(_LayerCall(fn, append_args, decode_args))
+        self._keep = (caches, q, key, value, out)
+
+    def append(self, layer: int) -> None:
+        c = self.calls[layer]
+        rc = c.append_fn(*c.append_args)
+        if rc:
+            _lib.check(rc, f"append layer {layer}")
+
+    def attend(self, layer: int) -> None:
+        rc = self.lib.wkv_paged_decode_gqa(*self.calls[layer].decode_args)
+        if rc:
+            _lib.check(rc, f"decode layer {layer}")
+
+    def run(self) -> None:
+        """One decode step: append then attend, layer by layer."""
+        for layer in range(len(self.calls)):
+            self.append(layer)
+            self.attend(layer)
