@@ -11,8 +11,9 @@ layers never hit in cache. Inputs are synthetic and already resident in HBM.
 
 Prints one JSON line:
   value        algorithmic bytes of a step / measured step time (GB/s)
-  roofline     the attention kernel: algorithmic bytes per launch / its mean
-               launch time (HIP events on the launch stream) vs 8 TB/s
+  roofline     one layer's fused append + attention launch: algorithmic bytes
+               per launch / its mean time (HIP events on the launch stream),
+               against the 8 TB/s HBM peak
   cpu_baseline the CPU oracle on a bounded sample of the same workload
 """
 
@@ -165,31 +166,31 @@ def main() -> int:
     print(f"# timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {t_wall / args.steps * 1e3:.2f} ms/step)",
           file=sys.stderr, flush=True)
 
-    # per-launch timing of the attention kernel, layer caches rotated
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(args.kernel_reps * args.layers)]
-    i = 0
-    for _ in range(args.kernel_reps):
-        for layer in range(args.layers):
-            a, b = pairs[i]
-            a.record()
-            step.attend(layer)
-            b.record()
-            i += 1
-    torch.cuda.synchronize()
-    kernel_us = float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3
-    apairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.layers)]
-    for layer, (a, b) in enumerate(apairs):
-        a.record()
-        step.append(layer)
-        b.record()
-    torch.cuda.synchronize()
-    append_us = float(np.mean([a.elapsed_time(b) for a, b in apairs])) * 1e3
+    # Per-launch timing of one layer's fused append + attention (the decode
+    # kernel and, when a context spans several partitions, its merge kernel),
+    # layer caches rotated so no layer is re-read from cache.
+    def per_launch(fn, reps):
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range(reps * args.layers)]
+        i = 0
+        for _ in range(reps):
+            for layer in range(args.layers):
+                a, b = pairs[i]
+                a.record()
+                fn(layer)
+                b.record()
+                i += 1
+        torch.cuda.synchronize()
+        return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3
+
+    kernel_us = per_launch(step.step_layer, args.kernel_reps)
+    attend_us = per_launch(step.attend, 1)
+    append_us = per_launch(step.append, 1)
 
     by = algorithmic_bytes(B, L, HQ, HKV, D, BS)
     step_bytes = by["layer"] * args.layers
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    achieved = by["attention"] / (kernel_us * 1e-6) / 1e9
+    achieved = by["layer"] / (kernel_us * 1e-6) / 1e9
     rec = {
         "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx",
         "value": round(value, 2),
@@ -213,16 +214,16 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_gqa_kernel<128,false>",
+            "kernel": "decode_gqa_kernel<128,false,true> (+ decode_merge_kernel<128>)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "bytes_per_launch": by["attention"],
+            "bytes_per_launch": by["layer"],
             "mean_launch_us": round(kernel_us, 2),
         },
-        "append_mean_launch_us": round(append_us, 2),
+        "unfused_us": {"append": round(append_us, 2), "attention": round(attend_us, 2)},
     }
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(args, HQ, HKV, D, BS, scale, by["layer"])

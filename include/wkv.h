@@ -134,13 +134,11 @@ int wkv_copy_blocks(const wkv_cache_t *cache, const int64_t *block_mapping, int6
  * num_kv_heads). q: [batch, num_q_heads, head_dim] bf16 (head_dim contiguous,
  * strides multiples of 8); out: [batch, num_q_heads, head_dim] bf16
  * contiguous. max_seq_len must be >= every seq_lens[b]. partition_size
- * (tokens, multiple of 16; 0 = library choice) splits long contexts into
- * partitions; the last partition of each (sequence, KV head) to finish merges
- * them by log-sum-exp in the same launch. When a context spans several
- * partitions the call needs `workspace` (wkv_decode_workspace_size() bytes of
- * scratch) and `tickets`: >= batch * num_kv_heads int32 counters that are zero
- * on entry and that every call leaves zero again. Calls that share a tickets
- * buffer must be ordered on one stream. A zero-length sequence gives zeros.
+ * (tokens, multiple of 16 spanning at most 64 blocks; 0 = library choice)
+ * splits long contexts into partitions; a second kernel merges them by
+ * log-sum-exp, using `workspace` (wkv_decode_workspace_size() bytes of
+ * scratch; unused when every context fits one partition). A zero-length
+ * sequence gives zeros.
  * Replaces vLLM paged_attention_v1/v2 and the ROCm paged-attention op (decode
  * step of llm.generate, engine.py:887; semantics of attention.py:89-96 and the
  * attention_interface call at wavelet/kernels/patch.py:182-196). */
@@ -151,7 +149,26 @@ int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stri
                          void *out, int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
                          int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
                          int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
-                         int64_t workspace_bytes, int32_t *tickets, int64_t num_tickets, void *stream);
+                         int64_t workspace_bytes, void *stream);
+
+/* One whole decode step of one layer in one launch: append token b of
+ * key/value ([batch, num_kv_heads, head_dim] bf16) at slot_mapping[b] (-1 =
+ * none) -- bf16 as wkv_append, fp8 as wkv_append_fp8 with runs of one -- then
+ * the attention of wkv_paged_decode_gqa over contexts that include it.
+ * slot_mapping[b] must address position seq_lens[b] - 1 of sequence b, and
+ * partition_size (when given) must be a multiple of block_size. A slot of -1
+ * stores nothing, and what the attention then sees at that position is
+ * unspecified (meant for padding entries whose output is discarded). Equivalent to
+ * wkv_append (or wkv_append_fp8) followed by wkv_paged_decode_gqa; the append
+ * and attention the reference runs back to back per layer in its decode step
+ * (past_key_values.update then attention_interface, patch.py:173-196). */
+int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                int64_t value_stride_h, const int64_t *slot_mapping, const void *q,
+                                int64_t q_stride_b, int64_t q_stride_h, void *out, int32_t num_q_heads,
+                                const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                                int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Weight-absorbed MLA decode over the latent cache:
  *   s = (q_nope . c_kv + q_pe . k_pe) * scale; o = softmax(s) . c_kv

@@ -16,10 +16,9 @@ import ctypes
 import torch
 
 from . import _lib
-from .cache import MLALatentCache, PagedKVCache, _require_cuda, _stream, check_tables
+from .cache import MLALatentCache, PagedKVCache, _require_cuda, _slots, _stream, _token_rows, check_tables
 
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
-_tickets: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _key(device: torch.device) -> tuple[int, int]:
@@ -35,16 +34,6 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
-
-
-def _ticket_buffer(device: torch.device, n: int) -> torch.Tensor:
-    """Per-(device, stream) int32 merge tickets: zeroed once, left zero by every call."""
-    key = _key(device)
-    t = _tickets.get(key)
-    if t is None or t.numel() < n:
-        t = torch.zeros(max(n, 4096), dtype=torch.int32, device=device)
-        _tickets[key] = t
-    return t
 
 
 def _query(q: torch.Tensor, name: str, shape: tuple[int, ...], device: torch.device) -> torch.Tensor:
@@ -72,11 +61,18 @@ def paged_decode_gqa(
     max_seq_len: int | None = None,
     out: torch.Tensor | None = None,
     partition_size: int = 0,
+    new_key: torch.Tensor | None = None,
+    new_value: torch.Tensor | None = None,
+    slot_mapping: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One decode step of GQA attention: ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` bf16.
 
     Query head ``h`` reads KV head ``h // (Hq // Hkv)``. ``max_seq_len`` (a host
-    int, >= every ``seq_lens``) avoids a device sync when given.
+    int, >= every ``seq_lens``) avoids a device sync when given. With
+    ``new_key``/``new_value`` ``[B, Hkv, D]`` and ``slot_mapping [B]`` the step's
+    append is fused into the same launch: token ``b`` is written at
+    ``slot_mapping[b]`` (position ``seq_lens[b] - 1`` of sequence ``b``) before
+    attention reads it -- the same result as ``cache.append`` then this call.
     """
     if not isinstance(cache, PagedKVCache):
         raise ValueError("cache must be a PagedKVCache")
@@ -87,6 +83,16 @@ def paged_decode_gqa(
         raise ValueError(f"q must be [B={batch}, Hq, D]")
     hq = q.shape[1]
     q = _query(q, "q", (hq, cache.head_dim), dev)
+    fused = new_key is not None or new_value is not None or slot_mapping is not None
+    if fused:
+        if new_key is None or new_value is None or slot_mapping is None:
+            raise ValueError("a fused append needs new_key, new_value and slot_mapping together")
+        shape = (cache.num_kv_heads, cache.head_dim)
+        new_key = _token_rows(new_key, "new_key", shape, dev)
+        new_value = _token_rows(new_value, "new_value", shape, dev)
+        if new_key.shape[0] != batch or new_value.shape[0] != batch:
+            raise ValueError(f"new_key/new_value must hold one token per sequence ({batch})")
+        slot_mapping = _slots(slot_mapping, batch, dev)
     if out is None:
         out = torch.empty((batch, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, hq, cache.head_dim) or not out.is_contiguous():
@@ -99,12 +105,15 @@ def paged_decode_gqa(
     if need < 0:
         raise ValueError("invalid decode geometry")
     ws = _workspace(dev, need)
-    tk = _ticket_buffer(dev, batch * cache.num_kv_heads)
-    rc = lib.wkv_paged_decode_gqa(
-        ctypes.byref(cache.descriptor()), q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq,
-        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl,
-        float(scale), int(partition_size), ws.data_ptr(), ws.numel(), tk.data_ptr(), tk.numel(), _stream(dev),
-    )
+    tail = (q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq, block_table.data_ptr(),
+            block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl, float(scale),
+            int(partition_size), ws.data_ptr(), ws.numel(), _stream(dev))
+    if fused:
+        rc = lib.wkv_append_paged_decode_gqa(
+            ctypes.byref(cache.descriptor()), new_key.data_ptr(), new_key.stride(0), new_key.stride(1),
+            new_value.data_ptr(), new_value.stride(0), new_value.stride(1), slot_mapping.data_ptr(), *tail)
+    else:
+        rc = lib.wkv_paged_decode_gqa(ctypes.byref(cache.descriptor()), *tail)
     _lib.check(rc, "paged_decode_gqa")
     return out
 

@@ -22,77 +22,86 @@
 //             exactly the B operand, so P never leaves the lane)
 // fp8 caches are widened to bf16 in registers (exact) and their power-of-two
 // per-(block, head) scales are folded into the scores (K) and into P (V).
-// Long contexts are split into partitions (one wave each); the last wave of a
-// (sequence, KV head) to finish merges the partials by log-sum-exp, so one
-// launch does the whole step.
+// Long contexts are split into partitions (one wave each) whose partial
+// results a second, small kernel merges by log-sum-exp. (Merging inside the
+// main kernel needs device-scope release/acquire between waves of different
+// XCDs; measured here, that costs far more than the extra launch.)
+// The decode-step append can be fused in: the wave that owns a sequence's last
+// partition first writes the new token into the cache, then attends over it.
 #include <cmath>
 
 #include "wkv_common.h"
+#include "kv_append_dev.h"
 
 namespace wkv {
 
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short shortx4;
 
+// Registers of one 16-token tile exactly as loaded (fp8 is widened at use, so
+// issuing a tile never waits for its data).
 template <int D, bool FP8>
 struct Tile {
-  static constexpr int NQK = D / 32;  // QK MFMAs per tile
-  static constexpr int NPV = D / 16;  // PV MFMAs per tile
-  bf16x8 k[NQK];
-  shortx4 v[NPV];
+  static constexpr int NK = FP8 ? D / 64 : D / 32;  // 16-byte K loads per lane
+  static constexpr int NPV = D / 16;                 // PV MFMAs per tile
+  u32x4 k[NK];
+  u32x2 v[FP8 ? 1 : NPV];   // bf16: 4 tokens x 1 d per PV MFMA
+  uint32_t v8[FP8 ? NPV : 1];  // fp8: the same 4 tokens as 4 codes
+  int valid;                // tokens of the tile inside the sequence (0 = skip)
+  float ksc, vsc;           // fp8 per-(block, head) scales (1 for bf16)
 };
 
+__device__ __forceinline__ uint32_t f32x2_hi_halves(float lo, float hi) {
+  // e4m3 values are exact in bf16: the top half of the fp32 pattern is the bf16.
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
 __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-  // Each e4m3 value is exactly representable in bf16: widen through fp32 and
-  // keep the top half (truncation is exact here).
   u32x4 r;
-  const uint32_t w[2] = {lo, hi};
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w[q], false);
-    const floatx2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w[q], true);
-    r[2 * q] = __builtin_amdgcn_perm(__float_as_uint(a[1]), __float_as_uint(a[0]), 0x07060302u);
-    r[2 * q + 1] = __builtin_amdgcn_perm(__float_as_uint(b[1]), __float_as_uint(b[0]), 0x07060302u);
-  }
+  const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+  const floatx2 c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+  r[0] = f32x2_hi_halves(a[0], a[1]);
+  r[1] = f32x2_hi_halves(b[0], b[1]);
+  r[2] = f32x2_hi_halves(c[0], c[1]);
+  r[3] = f32x2_hi_halves(d[0], d[1]);
   return __builtin_bit_cast(bf16x8, r);
 }
 
 __device__ __forceinline__ shortx4 fp8x4_to_bf16x4(uint32_t w) {
-  const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
-  const floatx2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
   u32x2 r;
-  r[0] = __builtin_amdgcn_perm(__float_as_uint(a[1]), __float_as_uint(a[0]), 0x07060302u);
-  r[1] = __builtin_amdgcn_perm(__float_as_uint(b[1]), __float_as_uint(b[0]), 0x07060302u);
+  r[0] = f32x2_hi_halves(a[0], a[1]);
+  r[1] = f32x2_hi_halves(b[0], b[1]);
   return __builtin_bit_cast(shortx4, r);
 }
 
-// Loads one 16-token tile (tokens [o0, o0+16) of block blk) into registers.
+// Buffer-resource word 3 for raw (unformatted, unswizzled) buffers on gfx9-family parts.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// Issues the loads of one 16-token tile (tokens [o0, o0+16) of block blk) as
+// buffer loads: a wave-uniform resource (scalar registers) per (block, head)
+// region, a per-lane byte offset that never changes (koff, voff) and a scalar
+// offset per load, so no per-tile vector address arithmetic is needed.
 template <int D, bool FP8>
 __device__ __forceinline__ void load_tile(Tile<D, FP8> &t, const uint8_t *__restrict__ kc,
                                           const uint8_t *__restrict__ vc, int64_t blk, int kvh, int Hkv, int BS,
-                                          int o0, int col, int grp) {
-  if constexpr (!FP8) {
-    constexpr int C = D / 8;
-    const uint8_t *kb = kc + (((blk * Hkv + kvh) * C) * BS + o0 + col) * 16;
+                                          int o0, uint32_t koff, uint32_t voff) {
+  constexpr int X = FP8 ? 16 : 8;  // elements per 16-byte K chunk
+  constexpr int C = D / X;
+  constexpr int ESZ = FP8 ? 1 : 2;
+  const int region = D * BS * ESZ;  // bytes of one (block, head) region of K, and of V
+  const uint8_t *kb = kc + ((blk * Hkv + kvh) * C * BS + o0) * 16;
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(kb), 0, region, kRawBufferWord3);
 #pragma unroll
-    for (int j = 0; j < Tile<D, FP8>::NQK; ++j)
-      t.k[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(kb + (4 * j + grp) * BS * 16));
-    const uint8_t *vb = vc + (((blk * Hkv + kvh) * D + col) * BS + o0 + 4 * grp) * 2;
+  for (int j = 0; j < Tile<D, FP8>::NK; ++j)
+    t.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff, j * 4 * BS * 16, 0);
+  const uint8_t *vb = vc + ((blk * Hkv + kvh) * D * BS + o0) * ESZ;
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(vb), 0, region, kRawBufferWord3);
 #pragma unroll
-    for (int n = 0; n < Tile<D, FP8>::NPV; ++n)
-      t.v[n] = __builtin_bit_cast(shortx4, *reinterpret_cast<const u32x2 *>(vb + n * 16 * BS * 2));
-  } else {
-    constexpr int C = D / 16;
-    const uint8_t *kb = kc + (((blk * Hkv + kvh) * C) * BS + o0 + col) * 16;
-#pragma unroll
-    for (int m = 0; m < D / 64; ++m) {
-      const u32x4 raw = *reinterpret_cast<const u32x4 *>(kb + (4 * m + grp) * BS * 16);
-      t.k[2 * m] = fp8x8_to_bf16x8(raw[0], raw[1]);
-      t.k[2 * m + 1] = fp8x8_to_bf16x8(raw[2], raw[3]);
-    }
-    const uint8_t *vb = vc + ((blk * Hkv + kvh) * D + col) * BS + o0 + 4 * grp;
-#pragma unroll
-    for (int n = 0; n < Tile<D, FP8>::NPV; ++n)
-      t.v[n] = fp8x4_to_bf16x4(*reinterpret_cast<const uint32_t *>(vb + n * 16 * BS));
+  for (int n = 0; n < Tile<D, FP8>::NPV; ++n) {
+    if constexpr (FP8)
+      t.v8[n] = __builtin_amdgcn_raw_buffer_load_b32(vr, voff, n * 16 * BS, 0);
+    else
+      t.v[n] = __builtin_amdgcn_raw_buffer_load_b64(vr, voff, n * 16 * BS * 2, 0);
   }
 }
 
@@ -103,17 +112,26 @@ struct DecodeState {
   float l;  // this lane's share of the running denominator
 };
 
-// One tile of online-softmax attention. `valid` = tokens of the tile that
-// belong to the sequence (16 except in the last tile).
+// One tile of online-softmax attention.
 template <int D, bool FP8>
-__device__ __forceinline__ void attend_tile(DecodeState<D, FP8> &st, Tile<D, FP8> &t, const bf16x8 *qop,
-                                            float s_mul, float p_mul, int valid, int grp) {
+__device__ __forceinline__ void attend_tile(DecodeState<D, FP8> &st, const Tile<D, FP8> &t, const bf16x8 *qop,
+                                            float scale_log2, int grp) {
   floatx4 s = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (FP8) {
 #pragma unroll
-  for (int j = 0; j < Tile<D, FP8>::NQK; ++j) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(t.k[j], qop[j], s, 0, 0, 0);
+    for (int m = 0; m < D / 64; ++m) {
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(t.k[m][0], t.k[m][1]), qop[2 * m], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(t.k[m][2], t.k[m][3]), qop[2 * m + 1], s, 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j)
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, t.k[j]), qop[j], s, 0, 0, 0);
+  }
+  const float s_mul = scale_log2 * t.ksc;
   float sv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sv[i] = (4 * grp + i < valid) ? s[i] * s_mul : -INFINITY;
+  for (int i = 0; i < 4; ++i) sv[i] = (4 * grp + i < t.valid) ? s[i] * s_mul : -INFINITY;
   float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
   mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
   mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
@@ -125,50 +143,151 @@ __device__ __forceinline__ void attend_tile(DecodeState<D, FP8> &st, Tile<D, FP8
   for (int i = 0; i < 4; ++i) p[i] = exp2f(sv[i] - m_use);
   st.l = st.l * corr + ((p[0] + p[1]) + (p[2] + p[3]));
   st.m = m_new;
-#pragma unroll
-  for (int n = 0; n < D / 16; ++n) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) st.o[n][i] *= corr;
-  }
-  u32x2 pb;
-  pb[0] = f32_to_bf16_bits(p[0] * p_mul) | (f32_to_bf16_bits(p[1] * p_mul) << 16);
-  pb[1] = f32_to_bf16_bits(p[2] * p_mul) | (f32_to_bf16_bits(p[3] * p_mul) << 16);
-  const shortx4 pop = __builtin_bit_cast(shortx4, pb);
-  if (valid < 16) {
-    // Never let a masked slot's V reach the accumulator (it may hold NaN).
+  if (__any(corr != 1.f)) {  // the running max moved for some head: rescale
 #pragma unroll
     for (int n = 0; n < D / 16; ++n) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (4 * grp + e >= valid) t.v[n][e] = 0;
+      for (int i = 0; i < 4; ++i) st.o[n][i] *= corr;
     }
   }
+  u32x2 pb;
+  pb[0] = f32_to_bf16_bits(p[0] * t.vsc) | (f32_to_bf16_bits(p[1] * t.vsc) << 16);
+  pb[1] = f32_to_bf16_bits(p[2] * t.vsc) | (f32_to_bf16_bits(p[3] * t.vsc) << 16);
+  const shortx4 pop = __builtin_bit_cast(shortx4, pb);
 #pragma unroll
-  for (int n = 0; n < D / 16; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(t.v[n], pop, st.o[n], 0, 0, 0);
+  for (int n = 0; n < D / 16; ++n) {
+    shortx4 vop = FP8 ? fp8x4_to_bf16x4(t.v8[n]) : __builtin_bit_cast(shortx4, t.v[FP8 ? 0 : n]);
+    if (t.valid < 16) {
+      // Never let a masked slot's V reach the accumulator (it may hold NaN).
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (4 * grp + e >= t.valid) vop[e] = 0;
+    }
+    st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop, pop, st.o[n], 0, 0, 0);
+  }
 }
 
-template <int D, bool FP8>
-__global__ __launch_bounds__(64) void decode_gqa_kernel(
-    const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const float *__restrict__ ks,
-    const float *__restrict__ vs, const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
-    uint16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
-    int *__restrict__ counters, const int32_t *__restrict__ bt, int64_t bt_stride, int max_seq, const int32_t *__restrict__ seq_lens,
-    int Hq, int Hkv, int G, int BS, int64_t NB, float scale_log2, int P_tok, int max_parts) {
-  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
-  int L = seq_lens[b];
-  L = L < max_seq ? L : max_seq;  // max_seq <= block-table width * BS: every read stays in the table
-  const int nparts = L > 0 ? (L + P_tok - 1) / P_tok : 0;
-  if (nparts == 0) {
-    if (part == 0 && col < G) {  // empty context: zeros
-      uint16_t *op = out + (static_cast<int64_t>(b) * Hq + kvh * G + col) * D;
-#pragma unroll
-      for (int n = 0; n < D / 16; ++n) *reinterpret_cast<u32x2 *>(op + 16 * n + 4 * grp) = u32x2{0u, 0u};
-    }
-    return;
-  }
-  if (part >= nparts) return;
+// The new token of a fused append + decode step: token b of `key`/`value`
+// belongs to sequence b and goes to slot slots[b] (-1 = none).
+struct StepAppend {
+  const uint16_t *key;
+  int64_t kst, ksh;
+  const uint16_t *val;
+  int64_t vst, vsh;
+  const int64_t *slots;
+};
 
+// The token a bf16 fused append is adding, as a one-token tile built from
+// the step's inputs (spread one dword per lane in nk, nv) instead of the
+// cache, so the wave never waits for its own cache write.
+template <int D>
+__device__ __forceinline__ void new_token_tile(Tile<D, false> &t, uint32_t nk, uint32_t nv, int col, int grp) {
+  t.valid = 1;
+  t.ksc = 1.f;
+  t.vsc = 1.f;
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) {
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const uint32_t x = __shfl(nk, 4 * (4 * j + grp) + qd, 64);
+      t.k[j][qd] = col == 0 ? x : 0u;  // row 0 = the new token
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) {
+    const uint32_t x = __shfl(nv, (col + 16 * n) >> 1, 64);
+    const uint32_t h = (col & 1) ? (x >> 16) : (x & 0xffffu);
+    t.v[n][0] = grp == 0 ? h : 0u;  // token 0 of lane group 0
+    t.v[n][1] = 0u;
+  }
+}
+
+// Attention of one wave over tokens [t_begin, t_end) of sequence b: returns
+// the unnormalised output, running max and this lane's share of the sum.
+// `my_blk` holds, in lane i, the id of the partition's i-th block (loaded by
+// the caller; the host keeps a partition within 64 blocks); each tile takes
+// its id with a register readlane.
+template <int D, bool FP8>
+__device__ __forceinline__ void attend_partition(DecodeState<D, FP8> &st, const uint8_t *__restrict__ kc,
+                                                 const uint8_t *__restrict__ vc, const float *__restrict__ ks,
+                                                 const float *__restrict__ vs, const bf16x8 *qop, int my_blk,
+                                                 int t_begin, int t_end, int kvh, int Hkv, int BS, int64_t NB,
+                                                 float scale_log2, int lane, int col, int grp) {
+  if (t_end <= t_begin) return;
+  const int n_tiles = (t_end - t_begin + 15) / 16;
+  const int blk_first = t_begin / BS;
+  const int nblk = (t_end - 1) / BS - blk_first + 1;
+  float my_ks = 1.f, my_vs = 1.f;
+  if (lane >= nblk || my_blk < 0 || my_blk >= NB) my_blk = -1;  // -1: never read, its slots count as masked
+  if constexpr (FP8) {
+    if (my_blk >= 0) {
+      my_ks = ks[static_cast<int64_t>(my_blk) * Hkv + kvh];
+      my_vs = vs[static_cast<int64_t>(my_blk) * Hkv + kvh];
+    }
+  }
+  const uint32_t koff = static_cast<uint32_t>((grp * BS + col) * 16);
+  const uint32_t voff = static_cast<uint32_t>((col * BS + 4 * grp) * (FP8 ? 1 : 2));
+
+  // Issue tile i's loads unconditionally (an index past the end re-reads the
+  // last tile, an L2 hit) so the compiler can count outstanding loads and
+  // wait only for the tile about to be used: three tiles rotate, two in flight.
+  auto issue = [&](Tile<D, FP8> &t, int i) {
+    const int ii = i < n_tiles ? i : n_tiles - 1;
+    const int ts = t_begin + 16 * ii;
+    const int bi = ts / BS - blk_first;
+    int blk = __builtin_amdgcn_readlane(my_blk, bi);
+    t.valid = (i < n_tiles && blk >= 0) ? ((t_end - ts) < 16 ? (t_end - ts) : 16) : 0;
+    if constexpr (FP8) {
+      t.ksc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_ks), bi));
+      t.vsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_vs), bi));
+    } else {
+      t.ksc = 1.f;
+      t.vsc = 1.f;
+    }
+    if (blk < 0) blk = 0;
+    load_tile<D, FP8>(t, kc, vc, blk, kvh, Hkv, BS, ts % BS, koff, voff);
+  };
+  auto consume = [&](Tile<D, FP8> &t) { attend_tile<D, FP8>(st, t, qop, scale_log2, grp); };
+  // The loop body is straight-line: tiles past the end are issued and attended
+  // as fully masked (p = 0, V zeroed), which keeps the wait counts exact.
+  Tile<D, FP8> t0, t1, t2;
+  issue(t0, 0);
+  issue(t1, 1);
+  for (int i = 0; i < n_tiles; i += 3) {
+    issue(t2, i + 2);
+    consume(t0);
+    issue(t0, i + 3);
+    consume(t1);
+    issue(t1, i + 4);
+    consume(t2);
+  }
+}
+
+// Grid: (chunk, KV head, sequence); W waves per workgroup, wave w of chunk c
+// owns partition c*W + w of P_tok tokens. The waves of a workgroup merge
+// their partials through LDS; a context longer than one chunk leaves one
+// partial per chunk for decode_merge_kernel.
+template <int D, bool FP8, bool APPEND, int W>
+__global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
+    uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ ks, float *__restrict__ vs,
+    const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ out,
+    float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
+    int Mb, int max_seq, const int32_t *__restrict__ seq_lens, int Hq, int Hkv, int G, int BS, int64_t NB,
+    float scale_log2, int P_tok, int max_chunks, StepAppend ap) {
+  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // The wave index is uniform across the wave; saying so keeps everything
+  // derived from it (partition, block ids, buffer resources) in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int part = chunk * W + wave;
+  const int t_begin = part * P_tok;
+  const int blk_first = t_begin / BS;
+
+  // Loads that do not depend on the context length go out together with it:
+  // the partition's block ids (bounded by the block-table width) and q.
+  int L = seq_lens[b];
+  int my_blk = -1;
+  if (blk_first + lane < Mb) my_blk = bt[b * bt_stride + blk_first + lane];
   // Q^T operand: lane holds 8 d-values of head `col` (zero for padded heads).
   // The d order matches the K operand order of load_tile.
   bf16x8 qop[D / 32];
@@ -183,59 +302,87 @@ __global__ __launch_bounds__(64) void decode_gqa_kernel(
     }
   }
 
+  L = L < max_seq ? L : max_seq;  // max_seq <= block-table width * BS: every read stays in the table
+  const int nparts = L > 0 ? (L + P_tok - 1) / P_tok : 0;
+  const int nchunks = (nparts + W - 1) / W;
+  if (nparts == 0) {
+    if (chunk == 0 && wave == 0 && col < G) {  // empty context: zeros
+      uint16_t *op = out + (static_cast<int64_t>(b) * Hq + kvh * G + col) * D;
+#pragma unroll
+      for (int n = 0; n < D / 16; ++n) *reinterpret_cast<u32x2 *>(op + 16 * n + 4 * grp) = u32x2{0u, 0u};
+    }
+    return;
+  }
+  if (chunk >= nchunks) return;  // the whole workgroup leaves together
+  const bool active = part < nparts;
+  const bool owns_new = APPEND && part == nparts - 1;
+
+  // Fused append; the new token's block lies wholly in this wave's partition
+  // (the partition size is a multiple of the block size): no other wave reads it.
+  // fp8: a scale change can re-encode the whole block, so append first and
+  //      wait before the block is read back.
+  // bf16: the wave attends the cache up to the new token and then the token
+  //      itself from the step's inputs (held one dword per lane), writing it
+  //      to the cache at the end; nothing waits on the write or the slot.
+  uint32_t nk = 0, nv = 0;
+  int64_t slot = -1;
+  if constexpr (APPEND) {
+    if (owns_new) {
+      slot = ap.slots[b];
+      if constexpr (FP8) {
+        if (slot >= 0 && slot / BS < NB) {
+          const int64_t blk = slot / BS;
+          const int off = static_cast<int>(slot % BS);
+          fp8_append_one<D, false>(kc, ks, ap.key, ap.kst, ap.ksh, ap.slots, b, 1, blk, off, kvh, Hkv, BS);
+          fp8_append_one<D, true>(vc, vs, ap.val, ap.vst, ap.vsh, ap.slots, b, 1, blk, off, kvh, Hkv, BS);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      } else {
+        if (lane < D / 2) {
+          nk = reinterpret_cast<const uint32_t *>(ap.key + b * ap.kst + kvh * ap.ksh)[lane];
+          nv = reinterpret_cast<const uint32_t *>(ap.val + b * ap.vst + kvh * ap.vsh)[lane];
+        }
+      }
+    }
+  }
+
   DecodeState<D, FP8> st;
 #pragma unroll
   for (int n = 0; n < D / 16; ++n) st.o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
   st.m = -INFINITY;
   st.l = 0.f;
-
-  const int t_begin = part * P_tok;
-  const int t_end = (t_begin + P_tok) < L ? (t_begin + P_tok) : L;
-  const int32_t *btrow = bt + b * bt_stride;
-
-  // Block id of a tile; an out-of-range id turns the tile into masked slots.
-  auto tile_block = [&](int ts, int &valid) -> int64_t {
-    int64_t blk = btrow[ts / BS];
-    valid = (t_end - ts) < 16 ? (t_end - ts) : 16;
-    if (blk < 0 || blk >= NB) {
-      blk = 0;
-      valid = 0;
-    }
-    return blk;
-  };
-
-  Tile<D, FP8> ta, tb;
-  int va, vb;
-  int64_t ba = tile_block(t_begin, va), bb = 0;
-  load_tile<D, FP8>(ta, kc, vc, ba, kvh, Hkv, BS, t_begin % BS, col, grp);
-  for (int ts = t_begin; ts < t_end; ts += 32) {
-    const bool more = ts + 16 < t_end;
-    if (more) {
-      bb = tile_block(ts + 16, vb);
-      load_tile<D, FP8>(tb, kc, vc, bb, kvh, Hkv, BS, (ts + 16) % BS, col, grp);
-    }
-    {
-      const float ksc = FP8 ? ks[ba * Hkv + kvh] : 1.f;
-      const float vsc = FP8 ? vs[ba * Hkv + kvh] : 1.f;
-      attend_tile<D, FP8>(st, ta, qop, scale_log2 * ksc, vsc, va, grp);
-    }
-    if (!more) break;
-    if (ts + 32 < t_end) {
-      ba = tile_block(ts + 32, va);
-      load_tile<D, FP8>(ta, kc, vc, ba, kvh, Hkv, BS, (ts + 32) % BS, col, grp);
-    }
-    {
-      const float ksc = FP8 ? ks[bb * Hkv + kvh] : 1.f;
-      const float vsc = FP8 ? vs[bb * Hkv + kvh] : 1.f;
-      attend_tile<D, FP8>(st, tb, qop, scale_log2 * ksc, vsc, vb, grp);
+  if (active) {
+    const int t_end = (t_begin + P_tok) < L ? (t_begin + P_tok) : L;
+    const bool from_regs = APPEND && !FP8 && owns_new;  // last token comes from the inputs
+    attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, from_regs ? L - 1 : t_end, kvh, Hkv, BS,
+                             NB, scale_log2, lane, col, grp);
+    if constexpr (APPEND && !FP8) {
+      if (owns_new) {
+        Tile<D, FP8> tn;
+        new_token_tile<D>(tn, nk, nv, col, grp);
+        attend_tile<D, FP8>(st, tn, qop, scale_log2, grp);
+        // The cache write: lane i holds dword i of the K row and of the V row
+        // (d = 2i, 2i+1); nothing in this launch reads the slot back.
+        if (slot >= 0 && slot / BS < NB && lane < D / 2) {
+          const int64_t nblk_id = slot / BS;
+          const int off = static_cast<int>(slot % BS);
+          uint16_t *kd = reinterpret_cast<uint16_t *>(kc) +
+                         (((nblk_id * Hkv + kvh) * (D / 8) + (lane >> 2)) * BS + off) * 8 + (lane & 3) * 2;
+          *reinterpret_cast<uint32_t *>(kd) = nk;
+          uint16_t *vd = reinterpret_cast<uint16_t *>(vc) + ((nblk_id * Hkv + kvh) * D + 2 * lane) * BS + off;
+          vd[0] = static_cast<uint16_t>(nv & 0xffffu);
+          vd[BS] = static_cast<uint16_t>(nv >> 16);
+        }
+      }
     }
   }
-
   float l = st.l + __shfl_xor(st.l, 16, 64);
   l += __shfl_xor(l, 32, 64);
-  const int hq = kvh * G + col;
-  if (nparts == 1) {
-    if (col < G) {
+
+  if constexpr (W == 1) {
+    if (col >= G) return;
+    const int hq = kvh * G + col;
+    if (nparts == 1) {
       const float inv = l > 0.f ? 1.f / l : 0.f;
       uint16_t *op = out + (static_cast<int64_t>(b) * Hq + hq) * D;
 #pragma unroll
@@ -245,11 +392,9 @@ __global__ __launch_bounds__(64) void decode_gqa_kernel(
         w[1] = f32_to_bf16_bits(st.o[n][2] * inv) | (f32_to_bf16_bits(st.o[n][3] * inv) << 16);
         *reinterpret_cast<u32x2 *>(op + 16 * n + 4 * grp) = w;
       }
+      return;
     }
-    return;
-  }
-  if (col < G) {
-    const int64_t row = (static_cast<int64_t>(b) * Hq + hq) * max_parts + part;
+    const int64_t row = (static_cast<int64_t>(b) * Hq + hq) * max_chunks + chunk;
     float *po = part_o + row * D;
 #pragma unroll
     for (int n = 0; n < D / 16; ++n) *reinterpret_cast<floatx4 *>(po + 16 * n + 4 * grp) = st.o[n];
@@ -257,50 +402,93 @@ __global__ __launch_bounds__(64) void decode_gqa_kernel(
       part_ml[2 * row] = st.m;
       part_ml[2 * row + 1] = l;
     }
-  }
-
-  // The last partition of this (sequence, KV head) to finish merges all of
-  // them by log-sum-exp: release the partials, take a ticket, and only the
-  // holder of the final ticket acquires and reads them back.
-  __threadfence();
-  int ticket = 0;
-  if (lane == 0) ticket = atomicAdd(&counters[b * Hkv + kvh], 1);
-  ticket = __shfl(ticket, 0, 64);
-  if (ticket != nparts - 1) return;
-  __threadfence();
-  for (int e = lane; e < G * (D / 4); e += 64) {
-    const int h = e / (D / 4), d0 = (e % (D / 4)) * 4;
-    const int64_t row0 = (static_cast<int64_t>(b) * Hq + kvh * G + h) * max_parts;
-    float M = -INFINITY;
-    for (int p = 0; p < nparts; ++p)
-      M = fmaxf(M, __hip_atomic_load(&part_ml[2 * (row0 + p)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const float m_use = (M == -INFINITY) ? 0.f : M;
-    float den = 0.f, num[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < nparts; ++p) {
-      const float mp = __hip_atomic_load(&part_ml[2 * (row0 + p)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float lp = __hip_atomic_load(&part_ml[2 * (row0 + p) + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float w = exp2f(mp - m_use);
-      den += w * lp;
-      const float *po = part_o + (row0 + p) * D + d0;
+  } else {
+    // Merge the W waves' partials of every head through LDS.
+    __shared__ float sm_o[W][16][D];
+    __shared__ float sm_m[W][16], sm_l[W][16];
+    if (col < G) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) num[i] += w * __hip_atomic_load(po + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int n = 0; n < D / 16; ++n) *reinterpret_cast<floatx4 *>(&sm_o[wave][col][16 * n + 4 * grp]) = st.o[n];
+      if (grp == 0) {
+        sm_m[wave][col] = st.m;
+        sm_l[wave][col] = l;
+      }
     }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    u32x2 wv;
-    wv[0] = f32_to_bf16_bits(num[0] * inv) | (f32_to_bf16_bits(num[1] * inv) << 16);
-    wv[1] = f32_to_bf16_bits(num[2] * inv) | (f32_to_bf16_bits(num[3] * inv) << 16);
-    *reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(b) * Hq + kvh * G + h) * D + d0) = wv;
+    __syncthreads();
+    const bool final_out = nchunks == 1;
+    for (int e = threadIdx.x; e < G * D; e += 64 * W) {
+      const int h = e / D, d = e % D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w][h]);
+      const float m_use = (M == -INFINITY) ? 0.f : M;
+      float num = 0.f, den = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float f = exp2f(sm_m[w][h] - m_use);
+        num += f * sm_o[w][h][d];
+        den += f * sm_l[w][h];
+      }
+      const int hq = kvh * G + h;
+      if (final_out) {
+        out[(static_cast<int64_t>(b) * Hq + hq) * D + d] =
+            static_cast<uint16_t>(f32_to_bf16_bits(den > 0.f ? num / den : 0.f));
+      } else {
+        const int64_t row = (static_cast<int64_t>(b) * Hq + hq) * max_chunks + chunk;
+        part_o[row * D + d] = num;
+        if (d == 0) {
+          part_ml[2 * row] = M;
+          part_ml[2 * row + 1] = den;
+        }
+      }
+    }
   }
-  if (lane == 0) counters[b * Hkv + kvh] = 0;  // leave the ticket counter zeroed for the next call
 }
 
-static int choose_partition(int batch, int hkv, int max_seq_len) {
-  // Enough work items to fill 256 CUs several waves deep, but at least 256
-  // tokens per item so the partial-result traffic stays a few percent.
+// Log-sum-exp merge of the per-chunk partials of one (sequence, query head).
+template <int D>
+__global__ __launch_bounds__(D) void decode_merge_kernel(const float *__restrict__ part_o,
+                                                         const float *__restrict__ part_ml,
+                                                         uint16_t *__restrict__ out,
+                                                         const int32_t *__restrict__ seq_lens, int max_seq, int Hq,
+                                                         int P_tok, int max_parts) {
+  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  int L = seq_lens[b];
+  L = L < max_seq ? L : max_seq;
+  const int nparts = L > 0 ? (L + P_tok - 1) / P_tok : 0;
+  if (nparts <= 1) return;
+  const int64_t row0 = (static_cast<int64_t>(b) * Hq + hq) * max_parts;
+  float M = -INFINITY;
+  for (int p = 0; p < nparts; ++p) M = fmaxf(M, part_ml[2 * (row0 + p)]);
+  const float m_use = (M == -INFINITY) ? 0.f : M;
+  float num = 0.f, den = 0.f;
+  for (int p = 0; p < nparts; ++p) {
+    const float w = exp2f(part_ml[2 * (row0 + p)] - m_use);
+    den += w * part_ml[2 * (row0 + p) + 1];
+    num += w * part_o[(row0 + p) * D + d];
+  }
+  out[(static_cast<int64_t>(b) * Hq + hq) * D + d] =
+      static_cast<uint16_t>(f32_to_bf16_bits(den > 0.f ? num / den : 0.f));
+}
+
+// Tokens per partition when the caller leaves it to the library: enough
+// work items to give every CU a full complement of resident waves in about
+// one round (fewer, longer waves amortise the per-wave prologue and the
+// partial-result traffic), at least 128 tokens, a multiple of the block size
+// (the fused append relies on it), and at most 64 blocks (one lane each).
+static int choose_partition(int batch, int hkv, int max_seq_len, int BS, int D) {
+  const int64_t target_waves = D == 128 ? 2048 : 4096;
   const int64_t items = static_cast<int64_t>(batch) * hkv;
-  int p = 256;
-  while (p < 2048 && items * ((max_seq_len + 2 * p - 1) / (2 * p)) >= 4096) p *= 2;
-  return p;
+  int64_t p = (items * max_seq_len + target_waves - 1) / target_waves;
+  const int64_t unit = BS;  // a multiple of 16 already
+  p = (p + unit - 1) / unit * unit;
+  const int64_t lo = (128 + unit - 1) / unit * unit;
+  int64_t hi = 1024 / unit * unit;
+  if (hi < unit) hi = unit;
+  if (hi > 64 * unit) hi = 64 * unit;
+  if (p < lo) p = lo;
+  if (p > hi) p = hi;
+  return static_cast<int>(p);
 }
 
 }  // namespace wkv
@@ -310,18 +498,19 @@ using namespace wkv;
 extern "C" int64_t wkv_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim,
                                              int32_t max_seq_len, int32_t partition_size) {
   if (batch < 0 || num_q_heads <= 0 || head_dim <= 0 || max_seq_len < 0 || partition_size < 0) return -1;
-  if (partition_size == 0) partition_size = 256;  // smallest partition the library picks by itself
+  if (partition_size == 0) partition_size = 128;  // smallest partition the library picks by itself
   const int64_t max_parts = (static_cast<int64_t>(max_seq_len) + partition_size - 1) / partition_size;
   // partial outputs and (max, sum) per (sequence, query head, partition)
   return static_cast<int64_t>(batch) * num_q_heads * (max_parts > 0 ? max_parts : 1) * (head_dim + 2) * 4;
 }
 
-extern "C" int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stride_b,
-                                    int64_t q_stride_h, void *out, int32_t num_q_heads,
-                                    const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
-                                    const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
-                                    int32_t partition_size, void *workspace, int64_t workspace_bytes,
-                                    int32_t *tickets, int64_t num_tickets, void *stream) {
+namespace wkv {
+
+static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stride_b, int64_t q_stride_h, void *out,
+                         int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
+                         int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
+                         float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
+                         const StepAppend *ap, void *stream) {
   int rc = check_cache(cache, -1);
   if (rc) return rc;
   WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
@@ -340,42 +529,105 @@ extern "C" int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int
   WKV_CHECK_ARG(max_blocks_per_seq > 0 && bt_stride >= max_blocks_per_seq, "bad block table geometry");
   WKV_CHECK_ARG(max_seq_len >= 0, "max_seq_len must be >= 0");
   WKV_CHECK_ARG(std::isfinite(scale), "scale must be finite");
-  if (partition_size == 0) partition_size = choose_partition(batch, Hkv, max_seq_len);
-  WKV_CHECK_ARG(partition_size >= 16 && partition_size % 16 == 0, "partition_size must be a positive multiple of 16");
   const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
+  if (partition_size == 0) partition_size = choose_partition(batch, Hkv, max_seq, BS, D);
+  WKV_CHECK_ARG(partition_size >= 16 && partition_size % 16 == 0, "partition_size must be a positive multiple of 16");
+  WKV_CHECK_ARG((partition_size + BS - 17) / BS + 1 <= 64,
+                "partition_size %d spans more than 64 blocks of %d tokens", partition_size, BS);
+  if (ap != nullptr)
+    WKV_CHECK_ARG(partition_size % BS == 0, "a fused append needs partition_size %d to be a multiple of block_size %d",
+                  partition_size, BS);
   const int max_parts = max_seq > 0 ? (max_seq + partition_size - 1) / partition_size : 1;
-  WKV_CHECK_ARG(max_parts <= 65535, "too many partitions (%d)", max_parts);
-  const int64_t need = wkv_decode_workspace_size(batch, num_q_heads, D, max_seq, partition_size);
-  if (max_parts > 1) {
+  // Waves per workgroup: partitions of one context share a workgroup (and an
+  // LDS merge) up to 4 at a time; longer contexts leave per-chunk partials.
+  const int W = max_parts <= 1 ? 1 : (max_parts <= 2 ? 2 : 4);
+  const int max_chunks = (max_parts + W - 1) / W;
+  WKV_CHECK_ARG(max_chunks <= 65535, "too many partitions (%d)", max_parts);
+  const int64_t need = wkv_decode_workspace_size(batch, num_q_heads, D, max_seq, partition_size * W);
+  if (max_chunks > 1)
     WKV_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= need,
                   "workspace too small: need %lld bytes, got %lld", (long long)need, (long long)workspace_bytes);
-    WKV_CHECK_ARG(tickets != nullptr && num_tickets >= static_cast<int64_t>(batch) * Hkv,
-                  "tickets must hold batch * num_kv_heads = %lld zeroed int32 counters",
-                  (long long)batch * Hkv);
-  }
   float *part_o = static_cast<float *>(workspace);
-  float *part_ml = part_o ? part_o + static_cast<int64_t>(batch) * num_q_heads * max_parts * D : nullptr;
-  int *counters = tickets;
+  float *part_ml = part_o ? part_o + static_cast<int64_t>(batch) * num_q_heads * max_chunks * D : nullptr;
   const float scale_log2 = scale * 1.4426950408889634f;
   auto s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(max_parts), static_cast<unsigned>(Hkv), static_cast<unsigned>(batch));
-  auto kc = static_cast<const uint8_t *>(cache->k);
-  auto vc = static_cast<const uint8_t *>(cache->v);
+  const dim3 grid(static_cast<unsigned>(max_chunks), static_cast<unsigned>(Hkv), static_cast<unsigned>(batch));
+  auto kc = static_cast<uint8_t *>(cache->k);
+  auto vc = static_cast<uint8_t *>(cache->v);
   auto qq = static_cast<const uint16_t *>(q);
   auto oo = static_cast<uint16_t *>(out);
   const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
-#define WKV_DECODE(Dv, F8)                                                                                   \
-  decode_gqa_kernel<Dv, F8><<<grid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, qq, q_stride_b,    \
-                                                q_stride_h, oo, part_o, part_ml, counters, block_table,   \
-                                                bt_stride,                                                \
-                                                max_seq, seq_lens, num_q_heads, Hkv, G, BS,               \
-                                                cache->num_blocks, scale_log2, partition_size, max_parts)
+  const StepAppend none{nullptr, 0, 0, nullptr, 0, 0, nullptr};
+  const StepAppend apv = ap ? *ap : none;
+#define WKV_DECODE(Dv, F8, AP, Wv)                                                                              \
+  decode_gqa_kernel<Dv, F8, AP, Wv><<<grid, 64 * Wv, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, qq,       \
+                                                             q_stride_b, q_stride_h, oo, part_o, part_ml,      \
+                                                             block_table, bt_stride, max_blocks_per_seq,       \
+                                                             max_seq, seq_lens,                                \
+                                                             num_q_heads, Hkv, G, BS, cache->num_blocks,       \
+                                                             scale_log2, partition_size, max_chunks, apv)
+#define WKV_DECODE_W(Dv, F8, AP)   \
+  do {                             \
+    if (W == 1)                    \
+      WKV_DECODE(Dv, F8, AP, 1);   \
+    else if (W == 2)               \
+      WKV_DECODE(Dv, F8, AP, 2);   \
+    else                           \
+      WKV_DECODE(Dv, F8, AP, 4);   \
+  } while (0)
   if (D == 128) {
-    if (fp8) WKV_DECODE(128, true); else WKV_DECODE(128, false);
+    if (fp8) { if (ap) WKV_DECODE_W(128, true, true); else WKV_DECODE_W(128, true, false); }
+    else { if (ap) WKV_DECODE_W(128, false, true); else WKV_DECODE_W(128, false, false); }
   } else {
-    if (fp8) WKV_DECODE(64, true); else WKV_DECODE(64, false);
+    if (fp8) { if (ap) WKV_DECODE_W(64, true, true); else WKV_DECODE_W(64, true, false); }
+    else { if (ap) WKV_DECODE_W(64, false, true); else WKV_DECODE_W(64, false, false); }
   }
+#undef WKV_DECODE_W
 #undef WKV_DECODE
-  WKV_CHECK_LAUNCH("wkv_paged_decode_gqa");
+  WKV_CHECK_LAUNCH("paged decode");
+  if (max_chunks > 1) {
+    const dim3 mgrid(static_cast<unsigned>(num_q_heads), static_cast<unsigned>(batch));
+    if (D == 128)
+      decode_merge_kernel<128><<<mgrid, 128, 0, s>>>(part_o, part_ml, oo, seq_lens, max_seq, num_q_heads,
+                                                     partition_size * W, max_chunks);
+    else
+      decode_merge_kernel<64><<<mgrid, 64, 0, s>>>(part_o, part_ml, oo, seq_lens, max_seq, num_q_heads,
+                                                   partition_size * W, max_chunks);
+    WKV_CHECK_LAUNCH("paged decode merge");
+  }
   return WKV_OK;
+}
+
+}  // namespace wkv
+
+extern "C" int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stride_b,
+                                    int64_t q_stride_h, void *out, int32_t num_q_heads,
+                                    const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                    const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                                    int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream) {
+  return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
+                       max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
+                       workspace_bytes, nullptr, stream);
+}
+
+extern "C" int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                           int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                           int64_t value_stride_h, const int64_t *slot_mapping, const void *q,
+                                           int64_t q_stride_b, int64_t q_stride_h, void *out, int32_t num_q_heads,
+                                           const int32_t *block_table, int64_t bt_stride,
+                                           int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                                           int32_t max_seq_len, float scale, int32_t partition_size,
+                                           void *workspace, int64_t workspace_bytes, void *stream) {
+  WKV_CHECK_ARG(key && value && aligned16(key) && aligned16(value), "key/value must be non-NULL and 16-byte aligned");
+  WKV_CHECK_ARG(key_stride_t >= 0 && key_stride_h >= 0 && value_stride_t >= 0 && value_stride_h >= 0 &&
+                    (key_stride_t | key_stride_h | value_stride_t | value_stride_h) % 8 == 0,
+                "key/value strides must be non-negative multiples of 8");
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  if (cache != nullptr && cache->kv_dtype == WKV_KV_FP8_E4M3)
+    WKV_CHECK_ARG(cache->k_scale && cache->v_scale, "fp8 cache needs k_scale and v_scale");
+  const StepAppend ap{static_cast<const uint16_t *>(key), key_stride_t, key_stride_h,
+                      static_cast<const uint16_t *>(value), value_stride_t, value_stride_h, slot_mapping};
+  return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
+                       max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
+                       workspace_bytes, &ap, stream);
 }

@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import _ticket_buffer, _workspace
+from .attention import _workspace
 from .cache import PagedKVCache, check_tables
 
 
@@ -26,6 +26,7 @@ class _LayerCall:
     append_fn: object
     append_args: tuple
     decode_args: tuple
+    fused_args: tuple
 
 
 class DecodeStep:
@@ -34,7 +35,8 @@ class DecodeStep:
     ``caches[l]`` is layer ``l``'s cache; ``q[l]`` ``[B, Hq, D]``, ``key[l]`` /
     ``value[l]`` ``[T, Hkv, D]`` and ``out[l]`` ``[B, Hq, D]`` are the per-layer
     step buffers; ``block_table`` / ``seq_lens`` / ``slot_mapping`` are shared by
-    all layers (as in a paged engine, one table per sequence).
+    all layers (as in a paged engine, one table per sequence). ``slot_mapping[b]``
+    is the slot of sequence ``b``'s new token (one token per sequence).
     """
 
     def __init__(self, caches: list[PagedKVCache], q: list[torch.Tensor], key: list[torch.Tensor],
@@ -56,7 +58,6 @@ class DecodeStep:
         if need < 0:
             raise ValueError("invalid decode geometry")
         self.workspace = _workspace(dev, need)
-        self.tickets = _ticket_buffer(dev, batch * c0.num_kv_heads)
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.lib = lib
         self.calls: list[_LayerCall] = []
@@ -71,12 +72,14 @@ class DecodeStep:
             desc = ctypes.byref(cache.descriptor())
             append_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
                            vv.stride(1), slot_mapping.data_ptr(), slot_mapping.numel(), self.stream)
-            decode_args = (desc, qq.data_ptr(), qq.stride(0), qq.stride(1), oo.data_ptr(), hq,
-                           self.block_table.data_ptr(), self.block_table.stride(0), self.block_table.shape[1],
-                           self.seq_lens.data_ptr(), batch, int(max_seq_len), ctypes.c_float(scale),
-                           int(partition_size), self.workspace.data_ptr(), self.workspace.numel(),
-                           self.tickets.data_ptr(), self.tickets.numel(), self.stream)
-            self.calls.append(_LayerCall(fn, append_args, decode_args))
+            tail = (qq.data_ptr(), qq.stride(0), qq.stride(1), oo.data_ptr(), hq,
+                    self.block_table.data_ptr(), self.block_table.stride(0), self.block_table.shape[1],
+                    self.seq_lens.data_ptr(), batch, int(max_seq_len), ctypes.c_float(scale),
+                    int(partition_size), self.workspace.data_ptr(), self.workspace.numel(), self.stream)
+            decode_args = (desc, *tail)
+            fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
+                          vv.stride(1), slot_mapping.data_ptr(), *tail)
+            self.calls.append(_LayerCall(fn, append_args, decode_args, fused_args))
         self._keep = (caches, q, key, value, out)
 
     def append(self, layer: int) -> None:
@@ -90,8 +93,17 @@ class DecodeStep:
         if rc:
             _lib.check(rc, f"decode layer {layer}")
 
-    def run(self) -> None:
-        """One decode step: append then attend, layer by layer."""
+    def step_layer(self, layer: int) -> None:
+        """Append + attention of one layer in a single launch (plus the partition merge)."""
+        rc = self.lib.wkv_append_paged_decode_gqa(*self.calls[layer].fused_args)
+        if rc:
+            _lib.check(rc, f"append+decode layer {layer}")
+
+    def run(self, fused: bool = True) -> None:
+        """One decode step over every layer (fused append + attention by default)."""
         for layer in range(len(self.calls)):
-            self.append(layer)
-            self.attend(layer)
+            if fused:
+                self.step_layer(layer)
+            else:
+                self.append(layer)
+                self.attend(layer)
