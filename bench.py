@@ -42,7 +42,35 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-reps", type=int, default=2, help="passes over all layers for per-launch timing")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only copy 1 GiB device to device (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+def calibrate_copy() -> int:
+    """One plain 1 GiB device-to-device copy: reads 1 GiB and writes 1 GiB of HBM."""
+    import torch
+
+    a = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copied_bytes": a.numel() * 4}))
+    return 0
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_gqa_qwen3_4b_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch") and kernel in line:
+                    return int(line.split()[1])
+    except OSError:
+        pass
+    return None
 
 
 def algorithmic_bytes(batch: int, context: int, hq: int, hkv: int, d: int, bs: int, kv_bytes: int = 2) -> dict:
@@ -117,6 +145,8 @@ def cpu_baseline(args, hq, hkv, d, bs, scale, per_layer_bytes) -> dict:
 
 def main() -> int:
     args = parse()
+    if args.calibrate_copy:
+        return calibrate_copy()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); run it with --gpus 1", file=sys.stderr)
         return 2
@@ -214,12 +244,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_gqa_kernel<128,false,true> (+ decode_merge_kernel<128>)",
+            "kernel": "decode_gqa_kernel<128,false,true,4>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("decode_gqa_kernel<128,false,true,4>"),
             "bytes_per_launch": by["layer"],
             "mean_launch_us": round(kernel_us, 2),
         },

@@ -1,0 +1,102 @@
+"""Host-side block management (CPU only): sharing, copy-on-write, salted prefix reuse, metrics."""
+
+import re
+
+import numpy as np
+import pytest
+
+from wavelet_amd import BlockManager
+
+
+def test_capacity_and_metrics_lines_match_the_scraped_format():
+    m = BlockManager(2048, 16)
+    # tests/test_adaptive_concurrency.py:211-222 in the reference: 16 x 2048 = 32768 tokens
+    assert m.capacity_tokens == 32_768
+    text = m.metrics_text()
+    assert 'vllm:cache_config_info{block_size="16",num_gpu_blocks="2048"} 1' in text
+    labels = dict(re.findall(r'(\w+)="([^"]*)"', text))
+    assert int(labels["num_gpu_blocks"]) * int(labels["block_size"]) == 32_768
+    m.allocate("a", np.arange(100))
+    usage = float(re.search(r"vllm:kv_cache_usage_perc (\S+)", m.metrics_text()).group(1))
+    assert usage == pytest.approx(7 / 2048, abs=1e-6)
+
+
+def test_group_shares_whole_prompt_blocks_without_copies():
+    m = BlockManager(256, 16)
+    m.allocate("g0", np.arange(1024))  # 64 full blocks
+    for j in range(1, 8):
+        m.fork("g0", f"g{j}")
+    prompt = m.blocks_of("g0")
+    assert all(m.ref_count(b) == 8 for b in prompt)
+    slots, cow = m.append_slots([f"g{j}" for j in range(8)])
+    assert cow == []  # the prompt ends on a block boundary: every member opens a private block
+    blocks = slots // 16
+    assert len(set(blocks.tolist())) == 8 and not set(blocks.tolist()) & set(prompt)
+    assert np.all(slots % 16 == 0)
+    bt, lens = m.tables([f"g{j}" for j in range(8)])
+    assert np.all(lens == 1025) and np.all(bt[:, :64] == np.array(prompt))
+
+
+def test_partial_shared_block_is_copied_on_first_write():
+    m = BlockManager(64, 16)
+    m.allocate("p", np.arange(40))  # 2 full blocks + 8 tokens in a third
+    m.fork("p", "c1")
+    m.fork("p", "c2")
+    last = m.blocks_of("p")[2]
+    assert m.ref_count(last) == 3
+    slots, cow = m.append_slots(["c1", "c2", "p"])
+    # c1 and c2 each copy the shared partial block; p then owns the original alone
+    assert [src for src, _ in cow] == [last, last]
+    assert slots[2] == last * 16 + 8 and m.ref_count(last) == 1
+    for (src, dst), s in zip(cow, slots[:2]):
+        assert s == dst * 16 + 8 and m.ref_count(dst) == 1
+    assert m.blocks_of("c1")[:2] == m.blocks_of("p")[:2]
+
+
+def test_share_prefix_takes_the_first_blocks():
+    m = BlockManager(64, 16)
+    m.allocate("src", np.arange(50))
+    m.share_prefix("src", ["x", "y"], 2)
+    assert m.blocks_of("x") == m.blocks_of("src")[:2] and m.seq_len("y") == 32
+    with pytest.raises(ValueError):
+        m.share_prefix("src", ["z"], 9)
+
+
+def test_prefix_cache_is_keyed_by_salt_and_cleared_by_reset():
+    m = BlockManager(64, 16)
+    prompt = np.arange(70)
+    assert m.allocate("a", prompt, cache_salt="step-1") == 0
+    assert m.allocate("b", prompt, cache_salt="step-1") == 64  # 4 full blocks reused
+    assert m.blocks_of("b")[:4] == m.blocks_of("a")[:4]
+    assert m.allocate("c", prompt, cache_salt="step-2") == 0  # another policy step: no sharing
+    assert m.allocate("d", prompt) == 0  # no salt differs from any salt
+    m.free("a")
+    m.free("b")
+    assert m.allocate("e", prompt, cache_salt="step-1") == 64  # released blocks stay matchable
+    m.free("e")
+    m.reset_prefix_cache()
+    assert m.allocate("f", prompt, cache_salt="step-1") == 0
+
+
+def test_free_and_exhaustion():
+    m = BlockManager(4, 16)
+    m.allocate("a", np.arange(48))
+    with pytest.raises(MemoryError):
+        m.allocate("b", np.arange(1000, 1040))  # no prefix in common: needs 3 fresh blocks
+    assert m.num_free_blocks == 1  # the failed allocation gave its blocks back
+    m.free("a")
+    assert m.num_free_blocks == 4 and m.usage == 0.0
+    m2 = BlockManager(2, 16, enable_prefix_caching=False)
+    m2.allocate("a", np.arange(32))
+    with pytest.raises(MemoryError):
+        m2.append_slots(["a"])
+
+
+def test_cached_blocks_are_evicted_lru_when_space_runs_out():
+    m = BlockManager(4, 16)
+    m.allocate("a", np.arange(32), cache_salt="s")  # 2 indexed full blocks
+    m.free("a")
+    assert m.num_free_blocks == 4
+    m.allocate("b", np.arange(100, 164))  # needs all 4: evicts the cached ones
+    m.free("b")
+    assert m.allocate("c", np.arange(32), cache_salt="s") == 0

@@ -249,3 +249,73 @@ def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, 
             pr /= pr.sum(axis=1, keepdims=True)
             ref[i, h * g:(h + 1) * g] = pr @ vv[:, h]
     check_attention(paged.bf16_to_f32(bits_of(out)), ref, f"fused {kv_dtype}")
+
+
+def test_decode_matches_golden_output(cuda, golden_dir):
+    from golden import make_golden as mg
+
+    w, k, v, q = mg.gqa_decode_case()
+    got = _run_gqa(w, cuda, k, v, q)
+    check_attention(got, np.load(golden_dir / "gqa_decode.npz")["out"], "golden gqa")
+
+
+@pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
+def test_grpo_group_decode_with_block_manager(cuda, kv_dtype):
+    """A GRPO group end to end: one prompt (partial last block) shared by 8 members through the
+    block manager, copy-on-write of the shared partial block, three fused decode steps; caches
+    bit-exact against the oracle's, attention within tolerance."""
+    from wavelet_amd import BlockManager
+
+    H, HQ, D, BS, NB = 4, 28, 128, 16, 256
+    is_fp8 = kv_dtype == "fp8_e4m3"
+    m = BlockManager(NB, BS)
+    group = [f"m{j}" for j in range(8)]
+    prompt_len = 1000
+    m.allocate(group[0], np.arange(prompt_len), cache_salt="policy-3")
+    for g in group[1:]:
+        m.fork(group[0], g)
+    npdt = np.uint8 if is_fp8 else np.uint16
+    kc, vc = paged.empty_cache(NB, BS, H, D, dtype=npdt)
+    ks = np.zeros((NB, H), np.float32)
+    vs = np.zeros((NB, H), np.float32)
+    cache = PagedKVCache(NB, BS, H, D, kv_dtype=kv_dtype, device=cuda)
+    blocks = np.array(m.blocks_of(group[0]), np.int64)
+    pos = np.arange(prompt_len)
+    pslots = blocks[pos // BS] * BS + pos % BS
+    kp = synth.normal_bf16(synth.stream_key("grpo", kv_dtype, "pk"), (prompt_len, H, D))
+    vp = synth.normal_bf16(synth.stream_key("grpo", kv_dtype, "pv"), (prompt_len, H, D))
+    if is_fp8:
+        paged.append_fp8(kc, vc, ks, vs, kp, vp, pslots)
+    else:
+        paged.append_bf16(kc, vc, kp, vp, pslots)
+    cache.append(to_dev_bits(kp, BF16, cuda), to_dev_bits(vp, BF16, cuda), torch.from_numpy(pslots).to(cuda))
+    scale = 1 / math.sqrt(D)
+    for step in range(3):
+        slots, cow = m.append_slots(group)
+        assert (len(cow) == 7) == (step == 0)  # only the first write into the shared partial block copies
+        if cow:
+            pairs = np.array(cow, np.int64)
+            cache.copy_blocks(torch.from_numpy(pairs).to(cuda))
+            for s_, d_ in pairs:
+                kc[d_], vc[d_], ks[d_], vs[d_] = kc[s_], vc[s_], ks[s_], vs[s_]
+        bt, lens = m.tables(group)
+        kn = synth.normal_bf16(synth.stream_key("grpo", kv_dtype, step, "k"), (8, H, D))
+        vn = synth.normal_bf16(synth.stream_key("grpo", kv_dtype, step, "v"), (8, H, D))
+        q = synth.normal_bf16(synth.stream_key("grpo", kv_dtype, step, "q"), (8, HQ, D))
+        if is_fp8:
+            paged.append_fp8(kc, vc, ks, vs, kn, vn, slots)
+        else:
+            paged.append_bf16(kc, vc, kn, vn, slots)
+        out = paged_decode_gqa(to_dev_bits(q, BF16, cuda), cache, torch.from_numpy(bt).to(cuda),
+                               torch.from_numpy(lens).to(cuda), scale, new_key=to_dev_bits(kn, BF16, cuda),
+                               new_value=to_dev_bits(vn, BF16, cuda), slot_mapping=torch.from_numpy(slots).to(cuda))
+        assert np.array_equal(bits_of(cache.k), kc) and np.array_equal(bits_of(cache.v), vc), f"cache step {step}"
+        if is_fp8:
+            np.testing.assert_array_equal(cache.k_scale.cpu().numpy(), ks)
+            kf = fp8.dequantize(paged.k_logical(kc).reshape(NB, BS, H, D), ks[:, None, :, None])
+            vf = fp8.dequantize(paged.v_logical(vc), vs[:, None, :, None])
+        else:
+            kl, vl = paged.logical_kv(kc, vc)
+            kf, vf = paged.bf16_to_f32(kl), paged.bf16_to_f32(vl)
+        ref = paged.decode_gqa(paged.bf16_to_f32(q), kf, vf, bt, lens, scale)
+        check_attention(paged.bf16_to_f32(bits_of(out)), ref, f"grpo {kv_dtype} step {step}")

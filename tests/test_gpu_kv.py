@@ -167,3 +167,25 @@ def test_mla_append_bit_exact(cuda):
             lat[s // BS, s % BS, R:] = kpe[t]
     cache.append(to_dev_bits(kvc, BF16, cuda), to_dev_bits(kpe, BF16, cuda), torch.from_numpy(slots).to(cuda))
     np.testing.assert_array_equal(bits_of(cache.latent), lat)
+
+
+def test_append_gather_matches_golden_digests(cuda, golden_dir):
+    """The committed fixture: cache and gathered context digests after prefill + decode append."""
+    import json
+
+    from golden import make_golden as mg
+
+    w, pslots, kp, vp, nslots, kn, vn = mg.append_gather_case()
+    expected = json.loads((golden_dir / "outputs.json").read_text())["append_gather"]
+    assert synth.sha256_of(w.block_tables, w.context_lens, pslots, kp, vp, nslots, kn, vn) == expected["inputs"]
+    H, D, BS, NB = w.num_kv_heads, w.head_dim, w.block_size, w.num_blocks
+    kc, vc = paged.empty_cache(NB, BS, H, D, fill=0xFFFF)
+    cache = PagedKVCache(NB, BS, H, D, device=cuda)
+    _upload(cache, kc, vc)
+    for sl, k, v in ((pslots, kp, vp), (nslots, kn, vn)):
+        cache.append(to_dev_bits(k, BF16, cuda), to_dev_bits(v, BF16, cuda), torch.from_numpy(sl).to(cuda))
+    assert synth.sha256_of(bits_of(cache.k)) == expected["k_cache"]
+    assert synth.sha256_of(bits_of(cache.v)) == expected["v_cache"]
+    gk, gv = cache.gather(torch.from_numpy(w.block_tables).to(cuda), torch.from_numpy(w.context_lens).to(cuda))
+    assert synth.sha256_of(bits_of(gk)) == expected["gathered_k"]
+    assert synth.sha256_of(bits_of(gv)) == expected["gathered_v"]

@@ -10,9 +10,11 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
 """
 
 from .attention import paged_decode_gqa, paged_decode_mla
+from .blocks import BlockManager
 from .cache import MLALatentCache, PagedKVCache, validate_tables
 
 __all__ = [
+    "BlockManager",
     "MLALatentCache",
     "PagedKVCache",
     "paged_decode_gqa",
