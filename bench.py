@@ -35,7 +35,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--workload", default="qwen3-4b",
+                    choices=["qwen3-4b", "qwen3-4b-var", "qwen2.5-0.5b", "qwen2.5-7b-groups", "deepseek-v3-mla"],
+                    help="qwen3-4b is the headline; the others are the remaining measured shapes")
+    ap.add_argument("--layers", type=int, default=0, help="0 = the model's depth (8 rotated layers for MLA)")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--partition", type=int, default=0, help="tokens per split-K partition (0 = library choice)")
@@ -60,6 +63,25 @@ def calibrate_copy() -> int:
     return 0
 
 
+def copy_ceiling_gbs(torch, dev, nbytes: int = 1 << 30, buffers: int = 4, reps: int = 8) -> float:
+    """Device-to-device copy rate (read + write bytes / time) over rotating 1 GiB buffers."""
+    src = [torch.empty(nbytes // 4, dtype=torch.float32, device=dev) for _ in range(buffers)]
+    dst = [torch.empty_like(src[0]) for _ in range(buffers)]
+    for t in src:
+        t.fill_(1.0)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for r in range(reps):
+        dst[r % buffers].copy_(src[r % buffers])
+    b.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return gbs
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if any."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_gqa_qwen3_4b_pmc.md")
@@ -71,17 +93,6 @@ def measured_traffic(kernel: str):
     except OSError:
         pass
     return None
-
-
-def algorithmic_bytes(batch: int, context: int, hq: int, hkv: int, d: int, bs: int, kv_bytes: int = 2) -> dict:
-    """Per-layer bytes of the KV path, as the path must move them at minimum."""
-    kv = batch * context * 2 * hkv * d * kv_bytes  # K and V of every context token
-    qo = batch * hq * d * 2 * 2  # q in, o out (bf16)
-    bt = batch * ((context + bs - 1) // bs) * 4  # block-table entries read
-    sl = batch * 4  # seq_lens
-    attn = kv + qo + bt + sl
-    append = batch * 2 * hkv * d * (2 + kv_bytes) + batch * 8  # new K/V in + cache write + slots
-    return {"attention": attn, "append": append, "layer": attn + append}
 
 
 def cpu_baseline(args, hq, hkv, d, bs, scale, per_layer_bytes) -> dict:
@@ -143,6 +154,113 @@ def cpu_baseline(args, hq, hkv, d, bs, scale, per_layer_bytes) -> dict:
     }
 
 
+def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0):
+    """Per-layer caches (own memory per layer), step buffers and a DecodeStep plan."""
+    from wavelet_amd import PagedKVCache
+    from wavelet_amd.plan import DecodeStep
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    B, HQ, HKV, D, BS = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
+    caches, qs, ks, vs, outs = [], [], [], [], []
+    for _ in range(args.layers):
+        c = PagedKVCache(w.num_blocks, BS, HKV, D, kv_dtype=kv_dtype, device=dev)
+        if kv_dtype == "bf16":
+            c.k.normal_(generator=gen)
+            c.v.normal_(generator=gen)
+            if qkv_std != 1.0:
+                c.k.mul_(qkv_std)
+                c.v.mul_(qkv_std)
+        else:  # random finite e4m3 codes (no 0x7F/0xFF NaN codes) and power-of-two scales
+            for t in (c.k, c.v):
+                t.copy_(torch.randint(0, 256, t.shape, generator=gen, device=dev, dtype=torch.int32)
+                        .to(torch.uint8) & 0xF7)
+            c.k_scale.fill_(2.0 ** -8)
+            c.v_scale.fill_(2.0 ** -8)
+        caches.append(c)
+        qs.append((torch.randn((B, HQ, D), generator=gen, device=dev) * qkv_std).to(torch.bfloat16))
+        ks.append((torch.randn((B, HKV, D), generator=gen, device=dev) * qkv_std).to(torch.bfloat16))
+        vs.append((torch.randn((B, HKV, D), generator=gen, device=dev) * qkv_std).to(torch.bfloat16))
+        outs.append(torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev))
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.context_lens).to(dev)
+    slots = torch.from_numpy(w.new_token_slots()).to(dev)
+    step = DecodeStep(caches, qs, ks, vs, outs, bt, sl, slots, w.scale, max_seq_len=int(w.context_lens.max()),
+                      partition_size=args.partition)
+    return step, caches[0].nbytes
+
+
+def workload(args, torch, dev) -> dict:
+    """Builds the selected workload: plan, bytes, names (the default is the headline)."""
+    from wavelet_amd import MLALatentCache, synth
+    from wavelet_amd.plan import MLADecodeStep
+
+    name = args.workload
+    if name in ("qwen3-4b", "qwen3-4b-var"):
+        w = synth.qwen3_4b_workload(batch=args.batch, context=args.context if name == "qwen3-4b" else None)
+        args.layers = args.layers or 36
+        step, cache_bytes = _gqa_setup(torch, dev, args, w, "bf16")
+        kv_bytes = 2
+        desc = "Qwen3-4B decode step: 36 layers x (append 1 token/seq + GQA paged decode attention)"
+    elif name == "qwen2.5-0.5b":
+        w = synth.qwen25_05b_workload()
+        args.layers = args.layers or 24
+        step, cache_bytes = _gqa_setup(torch, dev, args, w, "bf16", qkv_std=1 / 8)
+        kv_bytes = 2
+        desc = "Qwen2.5-0.5B decode step: 24 layers x (append + GQA decode), 14 q / 2 kv heads, d=64"
+    elif name == "qwen2.5-7b-groups":
+        w = synth.qwen25_7b_group_workload()
+        args.layers = args.layers or 28
+        step, cache_bytes = _gqa_setup(torch, dev, args, w, "fp8_e4m3")
+        kv_bytes = 1
+        desc = "Qwen2.5-7B GRPO groups, fp8 KV: 28 layers x (fp8 append + GQA decode), 32 x 8 seqs, shared 1024-token prompts"
+    elif name == "deepseek-v3-mla":
+        w = synth.deepseek_v3_mla_workload()
+        args.layers = args.layers or 8
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1234)
+        B, H, R, P, BS = w.batch, w.num_q_heads, 512, 64, w.block_size
+        caches, qn, qp, kc, kp, outs = [], [], [], [], [], []
+        for _ in range(args.layers):
+            c = MLALatentCache(w.num_blocks, BS, R, P, device=dev)
+            c.latent.normal_(generator=gen)
+            caches.append(c)
+            qn.append(torch.randn((B, H, R), generator=gen, device=dev).to(torch.bfloat16))
+            qp.append(torch.randn((B, H, P), generator=gen, device=dev).to(torch.bfloat16))
+            kc.append(torch.randn((B, R), generator=gen, device=dev).to(torch.bfloat16))
+            kp.append(torch.randn((B, P), generator=gen, device=dev).to(torch.bfloat16))
+            outs.append(torch.empty((B, H, R), dtype=torch.bfloat16, device=dev))
+        step = MLADecodeStep(caches, qn, qp, kc, kp, outs, torch.from_numpy(w.block_tables).to(dev),
+                             torch.from_numpy(w.context_lens).to(dev), torch.from_numpy(w.new_token_slots()).to(dev),
+                             w.scale, max_seq_len=int(w.context_lens.max()), partition_size=args.partition)
+        cache_bytes = caches[0].latent.numel() * 2
+        L = w.context_lens.astype(np.int64)
+        attn = int(L.sum()) * (R + P) * 2 + B * H * (R + P) * 2 + B * H * R * 2 + int(((L + BS - 1) // BS).sum()) * 4 + B * 4
+        append = B * (R + P) * 2 * 2 + B * 8
+        flops = 2 * int(L.sum()) * H * (R + P + R)
+        return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
+                "kernel": "decode_mla_kernel<8> (+ mla_merge_kernel<512>)", "dtype": "bf16", "flops_per_layer": flops,
+                "cache_bytes": cache_bytes,
+                "desc": f"DeepSeek-V3 MLA decode: {args.layers} layers x (latent append + absorbed attention), "
+                        "128 heads, 512+64 latent, B=32, context 4096, block 64"}
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    L = w.context_lens.astype(np.int64)
+    B, HQ, HKV, D, BS = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
+    used = np.unique(np.concatenate([w.block_tables[i, :(int(L[i]) + BS - 1) // BS] for i in range(B)]))
+    kv_unique = len(used) * BS * 2 * HKV * D * kv_bytes  # physical blocks read (shared prompts counted once)
+    if w.group_size == 1:
+        kv_unique = int(L.sum()) * 2 * HKV * D * kv_bytes
+    scales = len(used) * 2 * HKV * 4 if kv_bytes == 1 else 0
+    attn = kv_unique + scales + B * HQ * D * 2 * 2 + int(((L + BS - 1) // BS).sum()) * 4 + B * 4
+    append = B * 2 * HKV * D * (2 + kv_bytes) + B * 8
+    return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
+            "kernel": f"decode_gqa_kernel<{D},{'true' if kv_bytes == 1 else 'false'},true,W>",
+            "dtype": "fp8_e4m3 KV, bf16 q/o" if kv_bytes == 1 else "bf16", "desc": desc,
+            "flops_per_layer": 4 * int(L.sum()) * HQ * D, "cache_bytes": cache_bytes,
+            "logical_kv_bytes": int(L.sum()) * 2 * HKV * D * kv_bytes}
+
+
 def main() -> int:
     args = parse()
     if args.calibrate_copy:
@@ -152,34 +270,13 @@ def main() -> int:
         return 2
     import torch
 
-    from wavelet_amd import PagedKVCache, synth
-    from wavelet_amd.plan import DecodeStep
-
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    B, L, HQ, HKV, D, BS = args.batch, args.context, 32, 8, 128, 16
-    scale = 1.0 / np.sqrt(D)
-    nb = B * ((L + BS - 1) // BS)
-    w = synth.make_decode_workload("bench-qwen3-4b", batch=B, num_kv_heads=HKV, num_q_heads=HQ, head_dim=D,
-                                   block_size=BS, context_lens=np.full(B, L), num_blocks=nb)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(1234)
-    caches, qs, ks, vs, outs = [], [], [], [], []
-    for _ in range(args.layers):
-        c = PagedKVCache(nb, BS, HKV, D, device=dev)
-        c.k.normal_(generator=gen)
-        c.v.normal_(generator=gen)
-        caches.append(c)
-        qs.append(torch.randn((B, HQ, D), generator=gen, device=dev).to(torch.bfloat16))
-        ks.append(torch.randn((B, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
-        vs.append(torch.randn((B, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
-        outs.append(torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev))
-    bt = torch.from_numpy(w.block_tables).to(dev)
-    sl = torch.from_numpy(w.context_lens).to(dev)
-    slots = torch.from_numpy(w.new_token_slots()).to(dev)
-    step = DecodeStep(caches, qs, ks, vs, outs, bt, sl, slots, scale, max_seq_len=L, partition_size=args.partition)
+    wl = workload(args, torch, dev)
+    step, w = wl["step"], wl["w"]
     torch.cuda.synchronize()
-    print(f"# setup done: {args.layers} layers x {caches[0].nbytes / 2**30:.2f} GiB cache", file=sys.stderr, flush=True)
+    print(f"# setup done: {wl['name']}, {args.layers} layers x {wl['cache_bytes'] / 2**30:.2f} GiB cache",
+          file=sys.stderr, flush=True)
 
     for _ in range(args.warmup):
         step.run()
@@ -196,8 +293,7 @@ def main() -> int:
     print(f"# timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {t_wall / args.steps * 1e3:.2f} ms/step)",
           file=sys.stderr, flush=True)
 
-    # Per-launch timing of one layer's fused append + attention (the decode
-    # kernel and, when a context spans several partitions, its merge kernel),
+    # Per-launch timing of one layer's step (fused append + attention for GQA),
     # layer caches rotated so no layer is re-read from cache.
     def per_launch(fn, reps):
         pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -216,13 +312,16 @@ def main() -> int:
     kernel_us = per_launch(step.step_layer, args.kernel_reps)
     attend_us = per_launch(step.attend, 1)
     append_us = per_launch(step.append, 1)
+    ceiling = copy_ceiling_gbs(torch, dev)
 
-    by = algorithmic_bytes(B, L, HQ, HKV, D, BS)
-    step_bytes = by["layer"] * args.layers
+    step_bytes = wl["layer_bytes"] * args.layers
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    achieved = by["layer"] / (kernel_us * 1e-6) / 1e9
+    achieved = wl["layer_bytes"] / (kernel_us * 1e-6) / 1e9
+    headline = wl["name"] == "qwen3-4b"
+    B = w.batch
     rec = {
-        "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx",
+        "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx" if headline
+        else f"decode-attn+KV-append GB/s & us/step, {wl['name']}",
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -234,29 +333,35 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (random bf16 K/V/q, seeded), resident in HBM",
+        "dtype": wl["dtype"],
+        "data": "synthetic (random K/V/q, seeded), resident in HBM",
         "config": {
-            "workload": "Qwen3-4B decode step: 36 layers x (append 1 token/seq + GQA paged decode attention)",
-            "layers": args.layers, "batch": B, "context": L, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
-            "block_size": BS, "kv_dtype": "bf16", "partition_size": args.partition or "auto",
-            "bytes_per_step": step_bytes,
+            "workload": wl["desc"],
+            "layers": args.layers, "batch": B, "context": int(w.context_lens.max()) if headline else
+            [int(w.context_lens.min()), int(w.context_lens.max())],
+            "q_heads": w.num_q_heads, "kv_heads": w.num_kv_heads, "head_dim": w.head_dim,
+            "block_size": w.block_size, "partition_size": args.partition or "auto", "bytes_per_step": step_bytes,
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_gqa_kernel<128,false,true,4>",
+            "kernel": wl["kernel"].replace(",W>", ",4>") if headline else wl["kernel"],
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("decode_gqa_kernel<128,false,true,4>"),
-            "bytes_per_launch": by["layer"],
+            "traffic": measured_traffic("decode_gqa_kernel<128,false,true,4>") if headline else None,
+            "bytes_per_launch": wl["layer_bytes"],
             "mean_launch_us": round(kernel_us, 2),
+            "tflops": round(wl["flops_per_layer"] / (kernel_us * 1e-6) / 1e12, 2),
         },
         "unfused_us": {"append": round(append_us, 2), "attention": round(attend_us, 2)},
+        "hbm_copy_gbs": round(ceiling, 1),
     }
-    if not args.no_cpu_baseline:
-        rec["cpu_baseline"] = cpu_baseline(args, HQ, HKV, D, BS, scale, by["layer"])
+    if "logical_kv_bytes" in wl and wl["w"].group_size > 1:
+        rec["config"]["logical_kv_bytes_per_layer"] = wl["logical_kv_bytes"]
+    if headline and not args.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline(args, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size, w.scale,
+                                           wl["layer_bytes"])
     print(json.dumps(rec), flush=True)
     return 0
 

@@ -107,3 +107,64 @@ class DecodeStep:
             else:
                 self.append(layer)
                 self.attend(layer)
+
+
+class MLADecodeStep:
+    """Pre-validated MLA decode for every layer: append one latent entry per
+    sequence, then weight-absorbed attention over the latent cache."""
+
+    def __init__(self, caches, q_nope: list[torch.Tensor], q_pe: list[torch.Tensor], kv_c: list[torch.Tensor],
+                 k_pe: list[torch.Tensor], out: list[torch.Tensor], block_table: torch.Tensor, seq_lens: torch.Tensor,
+                 slot_mapping: torch.Tensor, scale: float, max_seq_len: int, partition_size: int = 0) -> None:
+        c0 = caches[0]
+        dev = c0.device
+        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, c0.block_size)
+        if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+            raise ValueError("slot_mapping must be a contiguous int64 vector")
+        batch = self.seq_lens.shape[0]
+        heads = q_nope[0].shape[1]
+        lib = _lib.load()
+        need = lib.wkv_mla_workspace_size(batch, heads, c0.kv_lora_rank, max_seq_len, int(partition_size))
+        if need < 0:
+            raise ValueError("invalid MLA decode geometry")
+        self.workspace = _workspace(dev, need)
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+        self.lib = lib
+        self.calls = []
+        for layer, cache in enumerate(caches):
+            qn, qp, kc, kp, oo = q_nope[layer], q_pe[layer], kv_c[layer], k_pe[layer], out[layer]
+            for name, t, shape in (("q_nope", qn, (batch, heads, cache.kv_lora_rank)),
+                                   ("q_pe", qp, (batch, heads, cache.rope_dim)),
+                                   ("out", oo, (batch, heads, cache.kv_lora_rank)),
+                                   ("kv_c", kc, (slot_mapping.numel(), cache.kv_lora_rank)),
+                                   ("k_pe", kp, (slot_mapping.numel(), cache.rope_dim))):
+                if t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous() or t.device != dev:
+                    raise ValueError(f"layer {layer}: {name} must be a contiguous bfloat16 {shape} tensor on {dev}")
+            desc = ctypes.byref(cache.descriptor())
+            append_args = (desc, kc.data_ptr(), kc.stride(0), kp.data_ptr(), kp.stride(0), slot_mapping.data_ptr(),
+                           slot_mapping.numel(), self.stream)
+            decode_args = (desc, qn.data_ptr(), qn.stride(0), qn.stride(1), qp.data_ptr(), qp.stride(0), qp.stride(1),
+                           oo.data_ptr(), heads, self.block_table.data_ptr(), self.block_table.stride(0),
+                           self.block_table.shape[1], self.seq_lens.data_ptr(), batch, int(max_seq_len),
+                           ctypes.c_float(scale), int(partition_size), self.workspace.data_ptr(),
+                           self.workspace.numel(), self.stream)
+            self.calls.append((append_args, decode_args))
+        self._keep = (caches, q_nope, q_pe, kv_c, k_pe, out, slot_mapping)
+
+    def append(self, layer: int) -> None:
+        rc = self.lib.wkv_mla_append(*self.calls[layer][0])
+        if rc:
+            _lib.check(rc, f"mla append layer {layer}")
+
+    def attend(self, layer: int) -> None:
+        rc = self.lib.wkv_paged_decode_mla(*self.calls[layer][1])
+        if rc:
+            _lib.check(rc, f"mla decode layer {layer}")
+
+    def step_layer(self, layer: int) -> None:
+        self.append(layer)
+        self.attend(layer)
+
+    def run(self) -> None:
+        for layer in range(len(self.calls)):
+            self.step_layer(layer)
