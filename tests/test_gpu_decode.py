@@ -187,10 +187,18 @@ def test_decode_mla_deepseek_v3_shape(cuda):
     _mla_case(cuda, [4096, 4096, 4096, 4096], tag="dsv3")
 
 
-@pytest.mark.parametrize("heads", [16, 128])
+@pytest.mark.parametrize("heads", [16, 32, 64, 128])
 def test_decode_mla_edge_lengths(cuda, heads):
     for p in (64, 0):
         _mla_case(cuda, [0, 1, 17, 64, 65, 300, 1000], heads=heads, partition_size=p, tag=f"edge{heads}p{p}")
+
+
+@pytest.mark.parametrize("bs,partition", [(16, 32), (16, 0), (64, 96), (32, 160), (128, 32)])
+def test_decode_mla_block_sizes_and_partitions(cuda, bs, partition):
+    """32-token steps that straddle two blocks, partitions that start inside a block,
+    and tails that end inside a step (NaN in every slot no sequence owns)."""
+    _mla_case(cuda, [5, 31, 32, 33, 95, 96, 97, 333, 1024, 2047], bs=bs, partition_size=partition,
+              tag=f"bs{bs}p{partition}")
 
 
 @pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
