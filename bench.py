@@ -239,7 +239,7 @@ def workload(args, torch, dev) -> dict:
         append = B * (R + P) * 2 * 2 + B * 8
         flops = 2 * int(L.sum()) * H * (R + P + R)
         return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
-                "kernel": "decode_mla_kernel<4,1> x2 head groups (+ mla_merge_kernel)", "dtype": "bf16", "flops_per_layer": flops,
+                "kernel": "decode_mla_kernel<4> x2 head groups (+ mla_merge_kernel)", "dtype": "bf16", "flops_per_layer": flops,
                 "cache_bytes": cache_bytes,
                 "desc": f"DeepSeek-V3 MLA decode: {args.layers} layers x (latent append + absorbed attention), "
                         "128 heads, 512+64 latent, B=32, context 4096, block 64"}

@@ -160,6 +160,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
+// Maximum over the four 16-lane rows of a wave (lanes col, col + 16, col + 32,
+// col + 48), with the cross-row swaps of gfx950 (no LDS round trip).
+__device__ __forceinline__ float row_max4(float v) {
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+
 // Online softmax keeps a reference maximum per head and rescales the running
 // sum and output only when a step's maximum exceeds it by more than 2^TAU:
 // probabilities are exp2(s - ref) <= 2^TAU (exact in bf16's range and
@@ -202,34 +211,43 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const float *__restrict_
   *reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(b) * H + h) * R + d) = v;
 }
 
-// NW waves, HPB 16-head blocks per wave for QK: a workgroup owns HW = 16 *
-// NW * HPB of the H = HW * HG heads. The 1-D grid is laid out for the
-// dispatcher, which deals workgroup i to XCD i mod 8: work item k = (sequence,
-// partition) goes to XCD k mod 8, and its HG head groups are workgroups
-// 8 HG (k / 8) + 8 g + (k mod 8), i.e. on the same XCD and dispatched back
-// to back, so the second read of each latent tile is served by that XCD's L2.
-template <int NW, int HPB>
-__global__ __launch_bounds__(64 * NW, 1) void decode_mla_kernel(
+// A workgroup owns HW = 16 NQ of the H = HW * HG heads of one (sequence,
+// partition) and runs 2 NQ waves in two roles, one of each per SIMD:
+//   QK waves (w < NQ):  Q^T of heads 16 w .. 16 w + 15 in registers; compute
+//       S for step s + 1, the online softmax, and write P^T and the rescale
+//       factors of that step to LDS.
+//   PV waves (w >= NQ): the output accumulators of d-slice (w - NQ) for all
+//       HW heads; issue the LDS copies, rescale, and accumulate O for step s.
+// One barrier per step hands step s + 1's probabilities from the QK waves to
+// the PV waves, which consume them one step later -- so on every SIMD the QK
+// wave's softmax and bookkeeping overlap the PV wave's MFMAs and the two
+// waves' MFMAs interleave. Four 36 KB step buffers: the PV waves read step s,
+// the QK waves step s + 1, and steps s + 2 and s + 3 are in flight.
+//
+// The 1-D grid is laid out for the dispatcher, which deals workgroup i to XCD
+// i mod 8: work item k = (sequence, partition) goes to XCD k mod 8, and its HG
+// head groups are workgroups 8 HG (k / 8) + 8 g + (k mod 8), i.e. on the same
+// XCD and dispatched back to back, so the second read of each latent tile is
+// served by that XCD's L2.
+template <int NQ>
+__global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
     const uint16_t *__restrict__ lat, const uint16_t *__restrict__ qn, int64_t qn_sb, int64_t qn_sh,
     const uint16_t *__restrict__ qp, int64_t qp_sb, int64_t qp_sh, uint16_t *__restrict__ out,
     float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
     int Mb, int max_seq, const int32_t *__restrict__ seq_lens, int BS, int64_t NB, float scale_log2, int P_tok,
     int max_parts, int H, int batch) {
   using namespace mla;
-  constexpr int NHB = NW * HPB;     // head blocks of this workgroup
+  constexpr int NHB = NQ;           // 16-head blocks of this workgroup
   constexpr int HW = 16 * NHB;      // heads of this workgroup
-  constexpr int DSL = R / NW;       // PV d-slice per wave
-  constexpr int NDT = DSL / 16;     // PV d-tiles per wave
-  constexpr int NIW = NDMA / NW;    // copies every wave issues per step
-  constexpr int NEXTRA = NDMA % NW; // waves < NEXTRA issue one more
-  static_assert(DSL % 64 == 0, "d-slice must be a multiple of 64");
+  constexpr int DSL = R / NQ;       // PV d-slice per PV wave
+  constexpr int NDT = DSL / 16;     // PV d-tiles per PV wave
+  constexpr int NIW = NDMA / NQ;    // copies every PV wave issues per step
+  constexpr int NBUF = 4;
+  static_assert(NDMA % NQ == 0 && DSL % 64 == 0, "copy split / d-slice");
 
-  __shared__ __attribute__((aligned(16))) uint8_t buf0[STEPB];
-  __shared__ __attribute__((aligned(16))) uint8_t buf1[STEPB];
-  __shared__ __attribute__((aligned(16))) uint8_t buf2[STEPB];
-  __shared__ __attribute__((aligned(16))) uint8_t pt[NHB * 1024];  // P^T, [hb][g][col][8 bf16]
-  __shared__ __attribute__((aligned(16))) uint8_t qpe_s[NHB * 2 * 1024];  // Q^T rope part, [hb][j][g][col][8]
-  __shared__ float corr_s[HW];
+  __shared__ __attribute__((aligned(16))) uint8_t buf[NBUF][STEPB];
+  __shared__ __attribute__((aligned(16))) uint8_t pt[2][NHB * 1024];  // P^T per step parity, [hb][g][col][8 bf16]
+  __shared__ float corr_s[2][HW];                                     // rescale factors per step parity, [col][hb]
   __shared__ float lsum_s[HW];
   __shared__ float mrun_s[HW];
 
@@ -245,6 +263,8 @@ __global__ __launch_bounds__(64 * NW, 1) void decode_mla_kernel(
   const int part = __builtin_amdgcn_readfirstlane(item % max_parts);
   const int hbase = HW * (wg_r >> 3);  // first head of this workgroup
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const bool is_qk = wave < NQ;
+  const int role_w = is_qk ? wave : wave - NQ;  // QK: head block; PV: d-slice
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int t_begin = part * P_tok;
   const int blk_first = __builtin_amdgcn_readfirstlane(t_begin / BS);
@@ -255,11 +275,14 @@ __global__ __launch_bounds__(64 * NW, 1) void decode_mla_kernel(
   int L = __builtin_amdgcn_readfirstlane(seq_lens[b]);
   int my_blk = -1;  // lane i: id of the partition's i-th block
   if (blk_first + lane < Mb) my_blk = bt[b * bt_stride + blk_first + lane];
+  // Pinned here so the compiler waits for the load now: its first use is in
+  // the step loop, where that wait would also drain the copies in flight.
+  asm volatile("" : "+v"(my_blk));
   L = L < max_seq ? L : max_seq;
   const int nparts = L > 0 ? (L + P_tok - 1) / P_tok : 0;
   if (nparts == 0) {
     if (part == 0) {
-      for (int e = threadIdx.x; e < HW * R / 8; e += 64 * NW)
+      for (int e = threadIdx.x; e < HW * R / 8; e += 128 * NQ)
         reinterpret_cast<u32x4 *>(out + (static_cast<int64_t>(b) * H + hbase) * R)[e] = u32x4{0u, 0u, 0u, 0u};
     }
     return;
@@ -268,194 +291,67 @@ __global__ __launch_bounds__(64 * NW, 1) void decode_mla_kernel(
   const int t_end = (t_begin + P_tok) < L ? (t_begin + P_tok) : L;
   const int nsteps = (t_end - t_begin + STEP - 1) / STEP;
 
-  // ---- copy issue: this wave's share of one step's 36 wave-instructions.
-  // Per copy r of this wave: token t of the step and byte offset t * ROWB + chunk,
-  // packed as (t << 16) | offset (offsets are < 2^16), fixed for every step.
-  constexpr int NCP = NIW + (NEXTRA ? 1 : 0);
-  uint32_t cp_tok_off[NCP];
+  // The two roles run separate loops with the same barrier sequence
+  // (prologue, one per step, epilogue), so each role's registers are live
+  // only in its own branch.
+  if (!is_qk) {
+    // ------------------------------------------------------------ PV role
+    // Copies: PV wave p issues the step's wave-instructions p, p + NQ, ...;
+    // for each, the token of the step and its byte offset t * ROWB + chunk,
+    // packed as (t << 16) | offset (offsets are < 2^16), fixed for every step.
+    uint32_t cp_tok_off[NIW];
 #pragma unroll
-  for (int r = 0; r < NCP; ++r) {
-    const int p = 64 * (wave + NW * r) + lane;
-    const int t = p / CH;
-    cp_tok_off[r] = (static_cast<uint32_t>(t) << 16) | static_cast<uint32_t>(t * ROWB + ((p - CH * t) ^ swz(t)) * 16);
-  }
-  StepPos ipos{0, off_first};  // the next step to copy
-  StepPos cpos{0, off_first};  // the next step to compute
-  auto issue = [&](int s, uint8_t *dst) __attribute__((always_inline)) {
-    const StepSrc src = step_src(lat, ipos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
-    advance(ipos, BS);
-    const uint32_t dst0 = lds_addr(dst);
-    const uint32_t lo_lim = static_cast<uint32_t>(src.n_lo) << 16;
-    if (src.full) {
+    for (int r = 0; r < NIW; ++r) {
+      const int p = 64 * (role_w + NQ * r) + lane;
+      const int t = p / CH;
+      cp_tok_off[r] = (static_cast<uint32_t>(t) << 16) | static_cast<uint32_t>(t * ROWB + ((p - CH * t) ^ swz(t)) * 16);
+    }
+    StepPos ipos{0, off_first};  // the next step to copy
+    auto issue = [&](int s) __attribute__((always_inline)) {
+      const StepSrc src = step_src(lat, ipos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
+      advance(ipos, BS);
+      const uint32_t dst0 = lds_addr(&buf[s & (NBUF - 1)][0]);
+      const uint32_t lo_lim = static_cast<uint32_t>(src.n_lo) << 16;
+      if (src.full) {
 #pragma unroll
-      for (int r = 0; r < NCP; ++r) {
-        if (r < NIW || wave < NEXTRA) {
+        for (int r = 0; r < NIW; ++r) {
           const uint32_t to = cp_tok_off[r];
-          copy16_to_lds((to < lo_lim ? src.base_lo : src.base_hi) + (to & 0xffffu), dst0 + 1024 * (wave + NW * r));
+          copy16_to_lds((to < lo_lim ? src.base_lo : src.base_hi) + (to & 0xffffu), dst0 + 1024 * (role_w + NQ * r));
         }
-      }
-    } else {
+      } else {
 #pragma unroll
-      for (int r = 0; r < NCP; ++r) {
-        if (r < NIW || wave < NEXTRA) {
+        for (int r = 0; r < NIW; ++r) {
           const uint32_t to = cp_tok_off[r];
           const int t = static_cast<int>(to >> 16);
           const int tc = token_ok(src, t) ? t : src.safe;
           // tc * ROWB + chunk offset, as a non-negative int (tc may be below t)
-          copy16_to_lds((tc < src.n_lo ? src.base_lo : src.base_hi) + (static_cast<int>(to & 0xffffu) + (tc - t) * ROWB),
-                        dst0 + 1024 * (wave + NW * r));
+          copy16_to_lds(
+              (tc < src.n_lo ? src.base_lo : src.base_hi) + (static_cast<int>(to & 0xffffu) + (tc - t) * ROWB),
+              dst0 + 1024 * (role_w + NQ * r));
         }
       }
-    }
-  };
+    };
 
-  // The first two steps' copies go out first, then Q. Q is then pinned
-  // (an empty asm that reads every Q register) before the loop, so the
-  // compiler waits for it here instead of inside the loop, where its count of
-  // vector-memory operations (it cannot see the copies) would also wait for
-  // every copy in flight.
-  issue(0, buf0);
-  if (nsteps > 1) issue(1, buf1);
-  // ---- Q^T operands: lane holds 8 elements of head 16*hb + col, k = 32 j + 8 grp.
-  // The c_kv part (j < 16) stays in registers; the rope part (j = 16, 17) is
-  // parked in LDS (each wave reads back only its own heads) to leave the
-  // registers to the accumulators and the LDS read pipeline.
-  constexpr int NJQ = R / 32;
-  bf16x8 qop[HPB][NJQ];
+    // Operand offsets. The transposed read of source lane (g, k, q) covers
+    // row 4 g + k, elements d0 + 4 q .. + 3 of this wave's d-slice.
+    const int tk = (lane >> 2) & 3, tq = lane & 3;
+    const int trow = 4 * grp + tk;
+    const int tr_row = trow * ROWB + role_w * DSL * 2 + (tq & 1) * 8;
+    const int tr_x = (tq >> 1) ^ swz(trow);  // chunk of d-tile a: (2 (a & 3) + (tq >> 1)) ^ swz = (2 (a & 3)) ^ tr_x
+    const int pt_w = ((grp * 16) + col) * 16;  // + hb * 1024
+    floatx4 acc[NDT][NHB];
 #pragma unroll
-  for (int hb = 0; hb < HPB; ++hb) {
-    const int hbg = wave * HPB + hb;
-    const int h = hbase + 16 * hbg + col;
+    for (int a = 0; a < NDT; ++a)
 #pragma unroll
-    for (int j = 0; j < NJQ; ++j)
-      qop[hb][j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qn + b * qn_sb + h * qn_sh + 32 * j + 8 * grp));
-#pragma unroll
-    for (int j = 0; j < PE / 32; ++j)
-      *reinterpret_cast<u32x4 *>(qpe_s + (hbg * 2 + j) * 1024 + (grp * 16 + col) * 16) =
-          *reinterpret_cast<const u32x4 *>(qp + b * qp_sb + h * qp_sh + 32 * j + 8 * grp);
-  }
-#pragma unroll
-  for (int hb = 0; hb < HPB; ++hb)
-#pragma unroll
-    for (int j = 0; j < NJQ; ++j) asm volatile("" : "+v"(qop[hb][j]));
+      for (int c = 0; c < NHB; ++c) acc[a][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    StepPos ppos{0, off_first};  // the next step to accumulate
 
-  // Per-lane LDS offsets. QK A operand: row (16 tt + col), chunk 4 j + grp.
-  const int sq = swz(col);
-  const int qk_gx = (grp ^ (sq & 3)) * 16 + col * ROWB;
-  const int qk_jb = (sq >> 2) * 64;  // chunk bit 2 flips j's bit 0
-  const int qk_even = qk_gx + qk_jb, qk_odd = qk_gx - qk_jb;
-  // PV A operand (transposed read): source lane (g, k, q) reads row 4 g + k,
-  // elements d0 + 4 q .. + 3 of its d-slice.
-  const int tk = (lane >> 2) & 3, tq = lane & 3;
-  const int trow = 4 * grp + tk;
-  const int tsw = swz(trow);
-  const int tr_row = trow * ROWB + wave * DSL * 2 + (tq & 1) * 8;
-  const int tr_x = (tq >> 1) ^ tsw;  // chunk of d-tile a: (2 (a & 3) + (tq >> 1)) ^ tsw = (2 (a & 3)) ^ tr_x
-  const int pt_w = ((grp * 16) + col) * 16;  // + hb * 1024
-
-  floatx4 acc[NDT][NHB];
-#pragma unroll
-  for (int a = 0; a < NDT; ++a)
-#pragma unroll
-    for (int c = 0; c < NHB; ++c) acc[a][c] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run[HPB], l_run[HPB];
-#pragma unroll
-  for (int hb = 0; hb < HPB; ++hb) {
-    m_run[hb] = -INFINITY;
-    l_run[hb] = 0.f;
-  }
-
-  auto step = [&](int s, const uint8_t *cur, uint8_t *nxt2) __attribute__((always_inline)) {
-    // Own copies of step s have landed once at most the next step's remain.
-    if (s + 1 < nsteps) {
-      if (NEXTRA && wave < NEXTRA)
-        wait_vmcnt<NIW + 1>();
-      else
-        wait_vmcnt<NIW>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    barrier_lds();
-    if (s + 2 < nsteps) issue(s + 2, nxt2);
-    const int ts = t_begin + STEP * s;
-    const StepSrc src = step_src(lat, cpos, ts, t_end, BS, my_blk, NBi);
-    advance(cpos, BS);
-
-    if (src.any) {
-      // ---- QK for this wave's heads over the step's 32 tokens. The A-operand
-      // reads run QKPF k-steps ahead of the MFMAs (a ring of register slots);
-      // the scheduling fences keep the compiler from sinking them back to
-      // their uses, which would leave one LDS round trip per MFMA.
-      constexpr int NJ = W / 32;
-      constexpr int QKPF = 2;
-      floatx4 sc[2][HPB];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int hb = 0; hb < HPB; ++hb) sc[tt][hb] = floatx4{0.f, 0.f, 0.f, 0.f};
-      bf16x8 ra[QKPF + 1][2];
-      auto qk_load = [&](int j) __attribute__((always_inline)) {
-        const int o = ((j & 1) ? qk_odd : qk_even) + 64 * j;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-          ra[j % (QKPF + 1)][tt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(cur + o + tt * HALF));
-      };
-#pragma unroll
-      for (int j = 0; j < QKPF; ++j) qk_load(j);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        if (j + QKPF < NJ) qk_load(j + QKPF);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int hb = 0; hb < HPB; ++hb) {
-          const bf16x8 qb = j < NJQ ? qop[hb][j < NJQ ? j : 0]
-                                    : __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                          qpe_s + ((wave * HPB + hb) * 2 + (j - NJQ)) * 1024 + pt_w));
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-            sc[tt][hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ra[j % (QKPF + 1)][tt], qb, sc[tt][hb], 0, 0, 0);
-        }
-      }
-      // ---- online softmax; lane (col, grp) holds tokens 4 grp + i and 16 + 4 grp + i.
-#pragma unroll
-      for (int hb = 0; hb < HPB; ++hb) {
-        float sv[8];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sv[4 * tt + i] = sc[tt][hb][i] * scale_log2;
-        if (!src.full) {
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (!token_ok(src, 16 * tt + 4 * grp + i)) sv[4 * tt + i] = -INFINITY;
-        }
-        float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        // m_run is the reference maximum (-inf until the first attended token).
-        const bool move = mt > m_run[hb] + TAU;
-        const float m_new = move ? mt : m_run[hb];
-        const float cr = (move && m_run[hb] != -INFINITY) ? fast_exp2(m_run[hb] - m_new) : 1.f;
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        float p[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
-        l_run[hb] = l_run[hb] * cr + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
-        m_run[hb] = m_new;
-        u32x4 pb;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pb[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
-        const int hbg = wave * HPB + hb;
-        *reinterpret_cast<u32x4 *>(pt + hbg * 1024 + pt_w) = pb;
-        if (grp == 0) corr_s[col * NHB + hbg] = cr;
-      }
-    }
-    barrier_lds();
-    if (src.any) {
-      // ---- PV: rescale, then O^T[d-slice, all heads] += C^T . P^T. The
-      // smaller operand set (d-tiles or head blocks) is held in registers.
+    auto pv_step = [&](int s) __attribute__((always_inline)) {
+      const StepSrc src = step_src(lat, ppos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
+      advance(ppos, BS);
+      if (!src.any) return;
+      const uint8_t *cur = &buf[s & (NBUF - 1)][0];
+      const uint8_t *pts = &pt[s & 1][0];
       typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s4;
       auto load_va = [&](int a) __attribute__((always_inline)) {
         const int o = tr_row + (((2 * (a & 3)) ^ tr_x) + 8 * (a >> 2)) * 16;
@@ -464,93 +360,189 @@ __global__ __launch_bounds__(64 * NW, 1) void decode_mla_kernel(
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)(cur + o + HALF));
         return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       };
-      float crs[NHB];  // rescale factors of heads 16 c + col, one LDS read batch
+      bf16x8 pb[NHB];
 #pragma unroll
-      for (int c = 0; c < NHB; ++c) crs[c] = corr_s[col * NHB + c];
-      auto rescale = [&](int c) __attribute__((always_inline)) {
-        const float cr = crs[c];
+      for (int c = 0; c < NHB; ++c) {
+        const float cr = corr_s[s & 1][col * NHB + c];  // rescale factor of head 16 c + col
+        pb[c] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(pts + c * 1024 + pt_w));
         if (__builtin_amdgcn_ballot_w64(cr != 1.f)) {
 #pragma unroll
           for (int a = 0; a < NDT; ++a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[a][c][i] *= cr;
         }
-      };
-      auto load_p = [&](int c) __attribute__((always_inline)) {
-        return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(pt + c * 1024 + pt_w));
-      };
-      if constexpr (NDT <= NHB) {
-        bf16x8 va[NDT];
+      }
+      // A-operand reads run PVPF d-tiles ahead of the MFMAs.
+      constexpr int PVPF = 2;
+      bf16x8 va[PVPF + 1];
 #pragma unroll
-        for (int a = 0; a < NDT; ++a) va[a] = load_va(a);
+      for (int a = 0; a < PVPF && a < NDT; ++a) va[a] = load_va(a);
 #pragma unroll
-        for (int c = 0; c < NHB; ++c) {
-          rescale(c);
-          const bf16x8 pb = load_p(c);
+      for (int a = 0; a < NDT; ++a) {
+        if (a + PVPF < NDT) va[(a + PVPF) % (PVPF + 1)] = load_va(a + PVPF);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int a = 0; a < NDT; ++a)
-            acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[a], pb, acc[a][c], 0, 0, 0);
-        }
-      } else {
-        bf16x8 pb[NHB];
+        for (int c = 0; c < NHB; ++c)
+          acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[a % (PVPF + 1)], pb[c], acc[a][c], 0, 0, 0);
+      }
+    };
+
+    const int n_pre = nsteps < 3 ? nsteps : 3;  // steps copied before the loop
+    for (int s = 0; s < n_pre; ++s) issue(s);
+    // Step 0 landed once at most the later prologue copies are pending (the
+    // counter holds 63: with one PV wave, wait for step 1 as well).
+    if (n_pre == 3)
+      wait_vmcnt<(2 * NIW < 64 ? 2 * NIW : NIW)>();
+    else if (n_pre == 2)
+      wait_vmcnt<NIW>();
+    else
+      wait_vmcnt<0>();
+    barrier_lds();  // step 0 visible to the QK waves
+    if (nsteps > 1) {
+      if (n_pre == 3)  // step 1 landed
+        wait_vmcnt<NIW>();
+      else
+        wait_vmcnt<0>();
+    }
+    for (int s = 0; s < nsteps; ++s) {
+      barrier_lds();  // P(s) written, step s + 1 landed, buffer of step s - 1 free
+      const bool more = s + 3 < nsteps;
+      if (more) issue(s + 3);
+      pv_step(s);
+      // Step s + 2 must have landed before the next barrier.
+      if (more)
+        wait_vmcnt<NIW>();
+      else
+        wait_vmcnt<0>();
+    }
+    __syncthreads();  // the QK waves' denominators and maxima are in LDS
+
+    // ---- epilogue: normalised output, or this partition's partials.
 #pragma unroll
-        for (int c = 0; c < NHB; ++c) {
-          rescale(c);
-          pb[c] = load_p(c);
-        }
+    for (int c = 0; c < NHB; ++c) {
+      const int hl = 16 * c + col, h = hbase + hl;
+      const float lh = lsum_s[hl];
 #pragma unroll
-        for (int a = 0; a < NDT; ++a) {
-          const bf16x8 va = load_va(a);
-#pragma unroll
-          for (int c = 0; c < NHB; ++c)
-            acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[c], acc[a][c], 0, 0, 0);
+      for (int a = 0; a < NDT; ++a) {
+        const int d0 = role_w * DSL + 16 * a + 4 * grp;
+        if (nparts == 1) {
+          const float inv = lh > 0.f ? 1.f / lh : 0.f;
+          u32x2 w;
+          w[0] = pack_bf16x2(acc[a][c][0] * inv, acc[a][c][1] * inv);
+          w[1] = pack_bf16x2(acc[a][c][2] * inv, acc[a][c][3] * inv);
+          *reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(b) * H + h) * R + d0) = w;
+        } else {
+          const int64_t row = (static_cast<int64_t>(b) * H + h) * max_parts + part;
+          *reinterpret_cast<floatx4 *>(part_o + row * R + d0) = acc[a][c];
         }
       }
+      if (nparts > 1 && role_w == 0 && grp == 0) {
+        const int64_t row = (static_cast<int64_t>(b) * H + h) * max_parts + part;
+        part_ml[2 * row] = mrun_s[hl];
+        part_ml[2 * row + 1] = lh;
+      }
     }
-  };
-
-  for (int s = 0; s < nsteps; s += 3) {
-    step(s, buf0, buf2);
-    if (s + 1 < nsteps) step(s + 1, buf1, buf0);
-    if (s + 2 < nsteps) step(s + 2, buf2, buf1);
+    return;
   }
 
-  // ---- epilogue: per-head denominators and maxima through LDS.
+  // -------------------------------------------------------------- QK role
+  // Q^T operand: lane holds 8 elements of head hbase + 16 w + col, k = 32 j + 8 grp.
+  constexpr int NJ = W / 32;
+  bf16x8 qop[NJ];
+  {
+    const int h = hbase + 16 * role_w + col;
 #pragma unroll
-  for (int hb = 0; hb < HPB; ++hb) {
-    float l = l_run[hb] + __shfl_xor(l_run[hb], 16, 64);
+    for (int j = 0; j < NJ; ++j) {
+      const uint16_t *src = (j < R / 32) ? qn + b * qn_sb + h * qn_sh + 32 * j + 8 * grp
+                                         : qp + b * qp_sb + h * qp_sh + 32 * (j - R / 32) + 8 * grp;
+      qop[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(src));
+    }
+  }
+  // Pin Q: the compiler waits for it here, not inside the loop.
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) asm volatile("" : "+v"(qop[j]));
+  float m_run = -INFINITY, l_run = 0.f;  // reference maximum (log2 domain) and this lane's share of the sum
+  StepPos qpos{0, off_first};  // the next step to score
+  const int sq = swz(col);
+  const int qk_gx = (grp ^ (sq & 3)) * 16 + col * ROWB;
+  const int qk_jb = (sq >> 2) * 64;  // chunk bit 2 flips j's bit 0
+  const int qk_even = qk_gx + qk_jb, qk_odd = qk_gx - qk_jb;
+  const int pt_w = ((grp * 16) + col) * 16;
+
+  auto qk_step = [&](int s) __attribute__((always_inline)) {
+    const StepSrc src = step_src(lat, qpos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
+    advance(qpos, BS);
+    if (!src.any) return;
+    const uint8_t *cur = &buf[s & (NBUF - 1)][0];
+    // S^T for the 32 tokens; A-operand reads run QKPF k-steps ahead (a ring
+    // of register slots; the scheduling fence keeps them there).
+    // Even and odd k-steps accumulate separately: four independent chains.
+    constexpr int QKPF = 2;
+    floatx4 sc[2][2] = {{floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}},
+                        {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}}};
+    bf16x8 ra[QKPF + 1][2];
+    auto qk_load = [&](int j) __attribute__((always_inline)) {
+      const int o = ((j & 1) ? qk_odd : qk_even) + 64 * j;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        ra[j % (QKPF + 1)][tt] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(cur + o + tt * HALF));
+    };
+#pragma unroll
+    for (int j = 0; j < QKPF; ++j) qk_load(j);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j + QKPF < NJ) qk_load(j + QKPF);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        sc[j & 1][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ra[j % (QKPF + 1)][tt], qop[j], sc[j & 1][tt], 0, 0, 0);
+    }
+    // Online softmax; lane (col, grp) holds tokens 4 grp + i and 16 + 4 grp + i.
+    float sv[8];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[4 * tt + i] = (sc[0][tt][i] + sc[1][tt][i]) * scale_log2;
+    if (!src.full) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (!token_ok(src, 16 * tt + 4 * grp + i)) sv[4 * tt + i] = -INFINITY;
+    }
+    const float mt = row_max4(
+        fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))));
+    const bool move = mt > m_run + TAU;
+    const float m_new = move ? mt : m_run;
+    const float cr = (move && m_run != -INFINITY) ? fast_exp2(m_run - m_new) : 1.f;
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
+    l_run = l_run * cr + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+    m_run = m_new;
+    u32x4 pbv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pbv[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+    *reinterpret_cast<u32x4 *>(&pt[s & 1][role_w * 1024 + pt_w]) = pbv;
+    if (grp == 0) corr_s[s & 1][col * NHB + role_w] = cr;
+  };
+
+  barrier_lds();  // step 0 landed
+  qk_step(0);
+  for (int s = 0; s < nsteps; ++s) {
+    barrier_lds();  // step s + 1 landed; the PV waves are done with P(s - 1)
+    if (s + 1 < nsteps) qk_step(s + 1);
+  }
+  {
+    float l = l_run + __shfl_xor(l_run, 16, 64);
     l += __shfl_xor(l, 32, 64);
     if (grp == 0) {
-      const int h = 16 * (wave * HPB + hb) + col;
-      lsum_s[h] = l;
-      mrun_s[h] = m_run[hb];
+      lsum_s[16 * role_w + col] = l;
+      mrun_s[16 * role_w + col] = m_run;
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int c = 0; c < NHB; ++c) {
-    const int hl = 16 * c + col, h = hbase + hl;
-    const float lh = lsum_s[hl];
-#pragma unroll
-    for (int a = 0; a < NDT; ++a) {
-      const int d0 = wave * DSL + 16 * a + 4 * grp;
-      if (nparts == 1) {
-        const float inv = lh > 0.f ? 1.f / lh : 0.f;
-        u32x2 w;
-        w[0] = f32_to_bf16_bits(acc[a][c][0] * inv) | (f32_to_bf16_bits(acc[a][c][1] * inv) << 16);
-        w[1] = f32_to_bf16_bits(acc[a][c][2] * inv) | (f32_to_bf16_bits(acc[a][c][3] * inv) << 16);
-        *reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(b) * H + h) * R + d0) = w;
-      } else {
-        const int64_t row = (static_cast<int64_t>(b) * H + h) * max_parts + part;
-        *reinterpret_cast<floatx4 *>(part_o + row * R + d0) = acc[a][c];
-      }
-    }
-    if (nparts > 1 && wave == 0 && grp == 0) {
-      const int64_t row = (static_cast<int64_t>(b) * H + h) * max_parts + part;
-      part_ml[2 * row] = mrun_s[hl];
-      part_ml[2 * row + 1] = lh;
-    }
-  }
 }
 
 // Blocks a partition of p tokens can touch: partitions start on a multiple
@@ -640,16 +632,15 @@ extern "C" int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_
   auto qn = static_cast<const uint16_t *>(q_nope);
   auto qpp = static_cast<const uint16_t *>(q_pe);
   auto oo = static_cast<uint16_t *>(out);
-#define WKV_MLA(NWv, HPBv)                                                                                       \
-  decode_mla_kernel<NWv, HPBv><<<grid, 64 * NWv, 0, s>>>(lat, qn, qn_stride_b, qn_stride_h, qpp, qp_stride_b,   \
-                                                         qp_stride_h, oo, part_o, part_ml, block_table, bt_stride, \
-                                                         max_blocks_per_seq, max_seq, seq_lens, BS,              \
-                                                         cache->num_blocks, scale_log2, partition_size, max_parts, \
-                                                         num_heads, batch)
+#define WKV_MLA(NQv)                                                                                        \
+  decode_mla_kernel<NQv><<<grid, 128 * NQv, 0, s>>>(lat, qn, qn_stride_b, qn_stride_h, qpp, qp_stride_b,          \
+                                                    qp_stride_h, oo, part_o, part_ml, block_table, bt_stride,      \
+                                                    max_blocks_per_seq, max_seq, seq_lens, BS, cache->num_blocks, \
+                                                    scale_log2, partition_size, max_parts, num_heads, batch)
   switch (num_heads) {
-    case 16: WKV_MLA(1, 1); break;
-    case 32: WKV_MLA(2, 1); break;
-    default: WKV_MLA(4, 1); break;  // 64 heads, or 128 as two head groups
+    case 16: WKV_MLA(1); break;
+    case 32: WKV_MLA(2); break;
+    default: WKV_MLA(4); break;  // 64 heads, or 128 as two head groups
   }
 #undef WKV_MLA
   WKV_CHECK_LAUNCH("wkv_paged_decode_mla");
