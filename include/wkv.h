@@ -186,6 +186,24 @@ int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64
                          int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
                          int64_t workspace_bytes, void *stream);
 
+/* One MLA decode step of one layer in one launch: latent[slot_mapping[b]] =
+ * concat(kv_c[b], k_pe[b]) (as wkv_mla_append; -1 = none), then the
+ * attention of wkv_paged_decode_mla over contexts that include that token.
+ * kv_c [batch, kv_lora_rank], k_pe [batch, rope_dim] bf16, row strides
+ * multiples of 8; slot_mapping[b] must address position seq_lens[b] - 1 of
+ * sequence b. The new token is attended from kv_c / k_pe (so nothing waits
+ * for its cache write). Equivalent to wkv_mla_append followed by
+ * wkv_paged_decode_mla: the latent append and MLA attention the engine runs
+ * back to back per layer (concat_and_cache_mla, then the MLA decode backend
+ * named at wavelet/inference/deepseek_v4.py:17, :64-66). */
+int wkv_append_paged_decode_mla(const wkv_mla_cache_t *cache, const void *kv_c, int64_t kv_c_stride,
+                                const void *k_pe, int64_t k_pe_stride, const int64_t *slot_mapping,
+                                const void *q_nope, int64_t qn_stride_b, int64_t qn_stride_h, const void *q_pe,
+                                int64_t qp_stride_b, int64_t qp_stride_h, void *out, int32_t num_heads,
+                                const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                                int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* ---- misc ---------------------------------------------------------------- */
 const char *wkv_last_error(void);
 int wkv_version(void);

@@ -119,6 +119,14 @@ def test_mla_rejects_unsupported_geometry():
     m = _lib.WkvMlaCache(latent=16, num_blocks=4, block_size=64, kv_lora_rank=512, rope_dim=64)
     rc = lib.wkv_paged_decode_mla(ctypes.byref(m), 16, 0, 0, 16, 0, 0, 16, 48, 16, 1, 1, 16, 1, 64, 0.1, 0, None, 0, None)
     assert rc == _lib.WKV_ERR_UNSUPPORTED
+    # fused append + decode: inputs checked before any launch
+    g = lib.wkv_append_paged_decode_mla
+    assert g(ctypes.byref(m), None, 512, 16, 64, 16, 16, 0, 0, 16, 0, 0, 16, 128, 16, 1, 1, 16, 1, 64, 0.1, 0, None, 0,
+             None) == _lib.WKV_ERR_INVALID
+    assert g(ctypes.byref(m), 16, 511, 16, 64, 16, 16, 0, 0, 16, 0, 0, 16, 128, 16, 1, 1, 16, 1, 64, 0.1, 0, None, 0,
+             None) == _lib.WKV_ERR_INVALID
+    assert g(ctypes.byref(m), 16, 512, 16, 64, None, 16, 0, 0, 16, 0, 0, 16, 128, 16, 1, 1, 16, 1, 64, 0.1, 0, None, 0,
+             None) == _lib.WKV_ERR_INVALID
 
 
 def test_workspace_sizes():

@@ -201,6 +201,49 @@ def test_decode_mla_block_sizes_and_partitions(cuda, bs, partition):
               tag=f"bs{bs}p{partition}")
 
 
+@pytest.mark.parametrize("heads,bs,partition", [(128, 64, 0), (16, 64, 96), (64, 16, 32), (32, 32, 0)])
+def test_fused_mla_append_decode_equals_append_then_decode(cuda, heads, bs, partition):
+    """One launch (latent append + MLA attention) leaves the cache bit-identical to
+    wkv_mla_append and attends within tolerance of the separate path and of the oracle; the new
+    token's slot and every unowned slot hold NaN before the step, so attending the new token from
+    the cache instead of its inputs, or reading past the context, shows up as NaN."""
+    R, P = 512, 64
+    lens = np.array([1, 2, 31, 32, 33, 64, 65, 300, 1024, 1025])
+    w = synth.make_decode_workload(f"fusedmla{heads}{bs}{partition}", batch=len(lens), num_kv_heads=1,
+                                   num_q_heads=heads, head_dim=R + P, block_size=bs, context_lens=lens,
+                                   scale=1 / math.sqrt(192.0))
+    own = _owned_mask(w)
+    ctx = w.context_lens.astype(np.int64)
+    new_slots = w.new_token_slots()
+    lat = synth.normal_bf16(synth.stream_key(w.name, "lat"), (w.num_blocks, bs, R + P))
+    lat[~own] = NAN16
+    lat.reshape(-1, R + P)[new_slots] = NAN16  # the appended token is not in the cache yet
+    caches = [MLALatentCache(w.num_blocks, bs, R, P, device=cuda) for _ in range(2)]
+    for c in caches:
+        c.latent.copy_(to_dev_bits(lat, BF16, cuda))
+    kvc_bits = synth.normal_bf16(synth.stream_key(w.name, "kvc"), (w.batch, R))
+    kpe_bits = synth.normal_bf16(synth.stream_key(w.name, "kpe"), (w.batch, P))
+    kvc, kpe = to_dev_bits(kvc_bits, BF16, cuda), to_dev_bits(kpe_bits, BF16, cuda)
+    q_bits = synth.normal_bf16(synth.stream_key(w.name, "q"), (w.batch, heads, R + P))
+    q = to_dev_bits(q_bits, BF16, cuda)
+    bt = torch.from_numpy(w.block_tables).to(cuda)
+    sl = torch.from_numpy(w.context_lens).to(cuda)
+    slots = torch.from_numpy(new_slots).to(cuda)
+    caches[0].append(kvc, kpe, slots)
+    ref_out = paged_decode_mla(q[:, :, :R], q[:, :, R:], caches[0], bt, sl, w.scale, partition_size=partition)
+    out = paged_decode_mla(q[:, :, :R], q[:, :, R:], caches[1], bt, sl, w.scale, partition_size=partition,
+                           new_kv_c=kvc, new_k_pe=kpe, slot_mapping=slots)
+    torch.cuda.synchronize()
+    assert torch.equal(caches[0].latent.view(torch.int16), caches[1].latent.view(torch.int16)), "latent differs"
+    torch.testing.assert_close(out.float(), ref_out.float(), atol=2e-2, rtol=1e-2)
+    full = lat.copy()
+    full.reshape(-1, R + P)[new_slots, :R] = kvc_bits
+    full.reshape(-1, R + P)[new_slots, R:] = kpe_bits
+    ref = paged.decode_mla(paged.bf16_to_f32(q_bits), paged.bf16_to_f32(full), w.block_tables, ctx, w.scale)
+    a, r = check_attention(paged.bf16_to_f32(bits_of(out)), ref, f"fused mla {heads}")
+    print(f"fused mla heads={heads} bs={bs} P={partition}: err abs {a:.2e} rel {r:.2e}")
+
+
 @pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("hq,hkv,d,bs", [(32, 8, 128, 16), (14, 2, 64, 16), (16, 4, 128, 64)])
 def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, d, bs):

@@ -129,8 +129,17 @@ def paged_decode_mla(
     max_seq_len: int | None = None,
     out: torch.Tensor | None = None,
     partition_size: int = 0,
+    new_kv_c: torch.Tensor | None = None,
+    new_k_pe: torch.Tensor | None = None,
+    slot_mapping: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Weight-absorbed MLA decode: ``q_nope [B, H, R]``, ``q_pe [B, H, P]`` -> ``[B, H, R]`` bf16."""
+    """Weight-absorbed MLA decode: ``q_nope [B, H, R]``, ``q_pe [B, H, P]`` -> ``[B, H, R]`` bf16.
+
+    With ``new_kv_c [B, R]``, ``new_k_pe [B, P]`` and ``slot_mapping [B]`` the
+    step's latent append is fused into the same launch: token ``b`` is written
+    at ``slot_mapping[b]`` (position ``seq_lens[b] - 1`` of sequence ``b``) and
+    attended -- the same result as ``cache.append`` then this call.
+    """
     if not isinstance(cache, MLALatentCache):
         raise ValueError("cache must be an MLALatentCache")
     dev = cache.device
@@ -143,6 +152,20 @@ def paged_decode_mla(
     q_pe = _query(q_pe, "q_pe", (heads, cache.rope_dim), dev)
     if q_pe.shape[0] != batch:
         raise ValueError("q_pe batch differs from q_nope")
+    fused = new_kv_c is not None or new_k_pe is not None or slot_mapping is not None
+    if fused:
+        if new_kv_c is None or new_k_pe is None or slot_mapping is None:
+            raise ValueError("a fused append needs new_kv_c, new_k_pe and slot_mapping together")
+        rows = []
+        for name, x, w in (("new_kv_c", new_kv_c, cache.kv_lora_rank), ("new_k_pe", new_k_pe, cache.rope_dim)):
+            _require_cuda(x, name, dev)
+            if x.dtype != torch.bfloat16 or x.dim() != 2 or tuple(x.shape) != (batch, w):
+                raise ValueError(f"{name} must be bfloat16 [{batch}, {w}]")
+            if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+                x = x.contiguous()
+            rows.append(x)
+        new_kv_c, new_k_pe = rows
+        slot_mapping = _slots(slot_mapping, batch, dev)
     if out is None:
         out = torch.empty((batch, heads, cache.kv_lora_rank), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, heads, cache.kv_lora_rank) or not out.is_contiguous():
@@ -155,11 +178,14 @@ def paged_decode_mla(
     if need < 0:
         raise ValueError("invalid MLA decode geometry")
     ws = _workspace(dev, need)
-    rc = lib.wkv_paged_decode_mla(
-        ctypes.byref(cache.descriptor()), q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1),
-        q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1), out.data_ptr(), heads,
-        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl,
-        float(scale), int(partition_size), ws.data_ptr(), ws.numel(), _stream(dev),
-    )
+    tail = (q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1), q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
+            out.data_ptr(), heads, block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+            seq_lens.data_ptr(), batch, msl, float(scale), int(partition_size), ws.data_ptr(), ws.numel(), _stream(dev))
+    if fused:
+        rc = lib.wkv_append_paged_decode_mla(
+            ctypes.byref(cache.descriptor()), new_kv_c.data_ptr(), new_kv_c.stride(0), new_k_pe.data_ptr(),
+            new_k_pe.stride(0), slot_mapping.data_ptr(), *tail)
+    else:
+        rc = lib.wkv_paged_decode_mla(ctypes.byref(cache.descriptor()), *tail)
     _lib.check(rc, "paged_decode_mla")
     return out

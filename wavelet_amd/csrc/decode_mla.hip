@@ -177,6 +177,17 @@ constexpr float TAU = 8.f;
 
 }  // namespace mla
 
+// The appended token of a fused append + decode step: row b of kv_c / k_pe
+// belongs to sequence b (its position seq_lens[b] - 1) and goes to slot
+// slots[b] (-1 = none). kvc == nullptr: attention only.
+struct MlaAppend {
+  const uint16_t *kvc;
+  int64_t kvc_st;
+  const uint16_t *kpe;
+  int64_t kpe_st;
+  const int64_t *slots;
+};
+
 // Log-sum-exp merge of the per-partition partials of one (sequence, head):
 // 128 lanes per head, four output elements (one 16-byte partial load per
 // partition) per lane, two heads per 256-thread workgroup.
@@ -231,11 +242,11 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const float *__restrict_
 // served by that XCD's L2.
 template <int NQ>
 __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
-    const uint16_t *__restrict__ lat, const uint16_t *__restrict__ qn, int64_t qn_sb, int64_t qn_sh,
+    uint16_t *__restrict__ lat, const uint16_t *__restrict__ qn, int64_t qn_sb, int64_t qn_sh,
     const uint16_t *__restrict__ qp, int64_t qp_sb, int64_t qp_sh, uint16_t *__restrict__ out,
     float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
     int Mb, int max_seq, const int32_t *__restrict__ seq_lens, int BS, int64_t NB, float scale_log2, int P_tok,
-    int max_parts, int H, int batch) {
+    int max_parts, int H, int batch, MlaAppend ap) {
   using namespace mla;
   constexpr int NHB = NQ;           // 16-head blocks of this workgroup
   constexpr int HW = 16 * NHB;      // heads of this workgroup
@@ -290,6 +301,12 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
   if (part >= nparts) return;
   const int t_end = (t_begin + P_tok) < L ? (t_begin + P_tok) : L;
   const int nsteps = (t_end - t_begin + STEP - 1) / STEP;
+  // Fused append: the partition holding position L - 1 attends the new token
+  // from the inputs (its step s_new, row tn) and head group 0 writes it to
+  // the cache; nothing in this launch reads that slot back.
+  const bool fuse = ap.kvc != nullptr && part == nparts - 1;
+  const int s_new = (L - 1 - t_begin) / STEP;
+  const int tn = (L - 1 - t_begin) - STEP * s_new;
 
   // The two roles run separate loops with the same barrier sequence
   // (prologue, one per step, epilogue), so each role's registers are live
@@ -312,7 +329,23 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
       advance(ipos, BS);
       const uint32_t dst0 = lds_addr(&buf[s & (NBUF - 1)][0]);
       const uint32_t lo_lim = static_cast<uint32_t>(src.n_lo) << 16;
-      if (src.full) {
+      if (fuse && s == s_new) {
+        // As the masked path, except that row tn (and every masked row that
+        // would copy it) comes from the appended token's inputs.
+        const uint8_t *kvc8 = reinterpret_cast<const uint8_t *>(ap.kvc + b * ap.kvc_st);
+        const uint8_t *kpe8 = reinterpret_cast<const uint8_t *>(ap.kpe + b * ap.kpe_st);
+#pragma unroll
+        for (int r = 0; r < NIW; ++r) {
+          const uint32_t to = cp_tok_off[r];
+          const int t = static_cast<int>(to >> 16);
+          const int tc = token_ok(src, t) ? t : src.safe;
+          const int off = static_cast<int>(to & 0xffffu);
+          const int c = (off - t * ROWB) >> 4;  // chunk of the row
+          const uint8_t *g = (tc < src.n_lo ? src.base_lo : src.base_hi) + (off + (tc - t) * ROWB);
+          if (tc == tn) g = c < R / 8 ? kvc8 + 16 * c : kpe8 + 16 * (c - R / 8);
+          copy16_to_lds(g, dst0 + 1024 * (role_w + NQ * r));
+        }
+      } else if (src.full) {
 #pragma unroll
         for (int r = 0; r < NIW; ++r) {
           const uint32_t to = cp_tok_off[r];
@@ -461,6 +494,16 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
   // Pin Q: the compiler waits for it here, not inside the loop.
 #pragma unroll
   for (int j = 0; j < NJ; ++j) asm volatile("" : "+v"(qop[j]));
+  if (fuse && hbase == 0 && role_w == 0) {  // the appended row -> its cache slot
+    const int64_t slot = ap.slots[b];
+    if (slot >= 0 && slot / BS < NB) {
+      uint16_t *dst = lat + slot * W;
+      for (int c = lane; c < CH; c += 64) {
+        const uint16_t *src = c < R / 8 ? ap.kvc + b * ap.kvc_st + 8 * c : ap.kpe + b * ap.kpe_st + 8 * (c - R / 8);
+        *reinterpret_cast<u32x4 *>(dst + 8 * c) = *reinterpret_cast<const u32x4 *>(src);
+      }
+    }
+  }
   float m_run = -INFINITY, l_run = 0.f;  // reference maximum (log2 domain) and this lane's share of the sum
   StepPos qpos{0, off_first};  // the next step to score
   const int sq = swz(col);
@@ -581,12 +624,14 @@ extern "C" int64_t wkv_mla_workspace_size(int32_t batch, int32_t num_heads, int3
   return static_cast<int64_t>(batch) * num_heads * (max_parts > 0 ? max_parts : 1) * (kv_lora_rank + 2) * 4;
 }
 
-extern "C" int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t qn_stride_b,
-                                    int64_t qn_stride_h, const void *q_pe, int64_t qp_stride_b, int64_t qp_stride_h,
-                                    void *out, int32_t num_heads, const int32_t *block_table, int64_t bt_stride,
-                                    int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
-                                    int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
-                                    int64_t workspace_bytes, void *stream) {
+namespace wkv {
+
+static int launch_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t qn_stride_b, int64_t qn_stride_h,
+                      const void *q_pe, int64_t qp_stride_b, int64_t qp_stride_h, void *out, int32_t num_heads,
+                      const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                      const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                      int32_t partition_size, void *workspace, int64_t workspace_bytes, const MlaAppend &ap,
+                      void *stream) {
   WKV_CHECK_ARG(cache != nullptr && cache->latent != nullptr && aligned16(cache->latent), "bad MLA cache");
   WKV_CHECK_ARG(cache->num_blocks > 0 && cache->num_blocks <= 0x7fffffff && cache->block_size > 0 &&
                     cache->block_size % 16 == 0 && cache->block_size <= 256,
@@ -628,7 +673,7 @@ extern "C" int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_
   const int64_t wgs = 8 * HG * ((items + 7) / 8);
   WKV_CHECK_ARG(wgs <= 0x7fffffff && items <= 0x7fffffff, "MLA grid too large");
   const dim3 grid(static_cast<unsigned>(wgs));
-  auto lat = static_cast<const uint16_t *>(cache->latent);
+  auto lat = static_cast<uint16_t *>(cache->latent);
   auto qn = static_cast<const uint16_t *>(q_nope);
   auto qpp = static_cast<const uint16_t *>(q_pe);
   auto oo = static_cast<uint16_t *>(out);
@@ -636,7 +681,7 @@ extern "C" int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_
   decode_mla_kernel<NQv><<<grid, 128 * NQv, 0, s>>>(lat, qn, qn_stride_b, qn_stride_h, qpp, qp_stride_b,          \
                                                     qp_stride_h, oo, part_o, part_ml, block_table, bt_stride,      \
                                                     max_blocks_per_seq, max_seq, seq_lens, BS, cache->num_blocks, \
-                                                    scale_log2, partition_size, max_parts, num_heads, batch)
+                                                    scale_log2, partition_size, max_parts, num_heads, batch, ap)
   switch (num_heads) {
     case 16: WKV_MLA(1); break;
     case 32: WKV_MLA(2); break;
@@ -650,4 +695,37 @@ extern "C" int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_
     WKV_CHECK_LAUNCH("wkv_paged_decode_mla merge");
   }
   return WKV_OK;
+}
+
+}  // namespace wkv
+
+extern "C" int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t qn_stride_b,
+                                    int64_t qn_stride_h, const void *q_pe, int64_t qp_stride_b, int64_t qp_stride_h,
+                                    void *out, int32_t num_heads, const int32_t *block_table, int64_t bt_stride,
+                                    int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                                    int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
+                                    int64_t workspace_bytes, void *stream) {
+  const MlaAppend none{nullptr, 0, nullptr, 0, nullptr};
+  return launch_mla(cache, q_nope, qn_stride_b, qn_stride_h, q_pe, qp_stride_b, qp_stride_h, out, num_heads,
+                    block_table, bt_stride, max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size,
+                    workspace, workspace_bytes, none, stream);
+}
+
+extern "C" int wkv_append_paged_decode_mla(const wkv_mla_cache_t *cache, const void *kv_c, int64_t kv_c_stride,
+                                           const void *k_pe, int64_t k_pe_stride, const int64_t *slot_mapping,
+                                           const void *q_nope, int64_t qn_stride_b, int64_t qn_stride_h,
+                                           const void *q_pe, int64_t qp_stride_b, int64_t qp_stride_h, void *out,
+                                           int32_t num_heads, const int32_t *block_table, int64_t bt_stride,
+                                           int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                                           int32_t max_seq_len, float scale, int32_t partition_size,
+                                           void *workspace, int64_t workspace_bytes, void *stream) {
+  WKV_CHECK_ARG(kv_c && k_pe && aligned16(kv_c) && aligned16(k_pe), "kv_c/k_pe must be non-NULL and 16-byte aligned");
+  WKV_CHECK_ARG(kv_c_stride >= 0 && k_pe_stride >= 0 && (kv_c_stride | k_pe_stride) % 8 == 0,
+                "kv_c/k_pe row strides must be non-negative multiples of 8");
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  const MlaAppend ap{static_cast<const uint16_t *>(kv_c), kv_c_stride, static_cast<const uint16_t *>(k_pe),
+                     k_pe_stride, slot_mapping};
+  return launch_mla(cache, q_nope, qn_stride_b, qn_stride_h, q_pe, qp_stride_b, qp_stride_h, out, num_heads,
+                    block_table, bt_stride, max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size,
+                    workspace, workspace_bytes, ap, stream);
 }

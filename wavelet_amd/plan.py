@@ -148,7 +148,9 @@ class MLADecodeStep:
                            self.block_table.shape[1], self.seq_lens.data_ptr(), batch, int(max_seq_len),
                            ctypes.c_float(scale), int(partition_size), self.workspace.data_ptr(),
                            self.workspace.numel(), self.stream)
-            self.calls.append((append_args, decode_args))
+            fused_args = (desc, kc.data_ptr(), kc.stride(0), kp.data_ptr(), kp.stride(0), slot_mapping.data_ptr(),
+                          *decode_args[1:])
+            self.calls.append((append_args, decode_args, fused_args))
         self._keep = (caches, q_nope, q_pe, kv_c, k_pe, out, slot_mapping)
 
     def append(self, layer: int) -> None:
@@ -162,8 +164,10 @@ class MLADecodeStep:
             _lib.check(rc, f"mla decode layer {layer}")
 
     def step_layer(self, layer: int) -> None:
-        self.append(layer)
-        self.attend(layer)
+        """Latent append + attention of one layer in a single launch (plus the partition merge)."""
+        rc = self.lib.wkv_append_paged_decode_mla(*self.calls[layer][2])
+        if rc:
+            _lib.check(rc, f"mla append+decode layer {layer}")
 
     def run(self) -> None:
         for layer in range(len(self.calls)):
