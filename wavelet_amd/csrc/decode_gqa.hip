@@ -131,19 +131,24 @@ __device__ __forceinline__ void attend_tile(DecodeState<D, FP8> &st, const Tile<
   const float s_mul = scale_log2 * t.ksc;
   float sv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sv[i] = (4 * grp + i < t.valid) ? s[i] * s_mul : -INFINITY;
-  float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-  mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-  mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-  const float m_new = fmaxf(st.m, mt);
+  for (int i = 0; i < 4; ++i) sv[i] = s[i] * s_mul;
+  if (t.valid < 16) {  // uniform: only a sequence's first and last tiles are partial
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * grp + i >= t.valid) sv[i] = -INFINITY;
+  }
+  const float mt = row_max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+  // st.m is the reference maximum (-inf until the first attended token).
+  const bool move = mt > st.m + SOFTMAX_TAU;
+  const float m_new = move ? mt : st.m;
+  const float corr = (move && st.m != -INFINITY) ? fast_exp2(st.m - m_new) : 1.f;
   const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-  const float corr = exp2f(st.m - m_use);
   float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = exp2f(sv[i] - m_use);
+  for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_use);
   st.l = st.l * corr + ((p[0] + p[1]) + (p[2] + p[3]));
   st.m = m_new;
-  if (__any(corr != 1.f)) {  // the running max moved for some head: rescale
+  if (__any(corr != 1.f)) {  // a reference maximum moved for some head: rescale
 #pragma unroll
     for (int n = 0; n < D / 16; ++n) {
 #pragma unroll
@@ -151,8 +156,8 @@ __device__ __forceinline__ void attend_tile(DecodeState<D, FP8> &st, const Tile<
     }
   }
   u32x2 pb;
-  pb[0] = f32_to_bf16_bits(p[0] * t.vsc) | (f32_to_bf16_bits(p[1] * t.vsc) << 16);
-  pb[1] = f32_to_bf16_bits(p[2] * t.vsc) | (f32_to_bf16_bits(p[3] * t.vsc) << 16);
+  pb[0] = pack_bf16x2(p[0] * t.vsc, p[1] * t.vsc);
+  pb[1] = pack_bf16x2(p[2] * t.vsc, p[3] * t.vsc);
   const shortx4 pop = __builtin_bit_cast(shortx4, pb);
 #pragma unroll
   for (int n = 0; n < D / 16; ++n) {

@@ -148,32 +148,7 @@ __device__ __forceinline__ bool token_ok(const StepSrc &s, int t) {
   return static_cast<bool>(static_cast<int>(t < s.lo_end) | (static_cast<int>(t >= s.n_lo) & static_cast<int>(t < s.hi_end)));
 }
 
-// 2^x on the hardware exp unit (v_exp_f32). Every argument here is <= 0 (a
-// score minus a running maximum), where the only difference from exp2f is
-// that results below 2^-126 flush to 0.
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Two fp32 -> packed bf16 (RNE) with the hardware conversion (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
-  typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
-}
-
-// Maximum over the four 16-lane rows of a wave (lanes col, col + 16, col + 32,
-// col + 48), with the cross-row swaps of gfx950 (no LDS round trip).
-__device__ __forceinline__ float row_max4(float v) {
-  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-}
-
-// Online softmax keeps a reference maximum per head and rescales the running
-// sum and output only when a step's maximum exceeds it by more than 2^TAU:
-// probabilities are exp2(s - ref) <= 2^TAU (exact in bf16's range and
-// precision), and rescaling -- a pass over every accumulator -- becomes rare.
-constexpr float TAU = 8.f;
 
 }  // namespace mla
 
@@ -555,7 +530,7 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
     }
     const float mt = row_max4(
         fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))));
-    const bool move = mt > m_run + TAU;
+    const bool move = mt > m_run + SOFTMAX_TAU;
     const float m_new = move ? mt : m_run;
     const float cr = (move && m_run != -INFINITY) ? fast_exp2(m_run - m_new) : 1.f;
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;

@@ -107,6 +107,38 @@ __device__ __forceinline__ uint32_t e4m3_quantize(float x, float scale) {
 }
 
 // ---------------------------------------------------------------------------
+// Attention arithmetic shared by the decode kernels.
+
+// 2^x on the hardware exp unit (v_exp_f32). Every argument these kernels pass
+// is <= 0 (a score minus a reference maximum), where the only difference from
+// exp2f is that results below 2^-126 flush to 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Two fp32 -> packed bf16 (RNE, NaN stays NaN) with the hardware conversion
+// (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+
+// Maximum over the four 16-lane rows of a wave (lanes c, c + 16, c + 32,
+// c + 48), with the cross-row swaps of gfx950 (no LDS round trip).
+__device__ __forceinline__ float row_max4(float v) {
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+
+// Online softmax keeps a reference maximum per query head and rescales the
+// running sum and output only when a tile's maximum exceeds it by more than
+// 2^SOFTMAX_TAU: probabilities are exp2(s - ref) <= 2^SOFTMAX_TAU (well inside
+// bf16's range, at its full precision), and a rescale -- a pass over every
+// accumulator -- becomes rare.
+constexpr float SOFTMAX_TAU = 8.f;
+
+// ---------------------------------------------------------------------------
 // Wavefront helpers (wave64).
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
