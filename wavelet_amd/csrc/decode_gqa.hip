@@ -50,27 +50,27 @@ struct Tile {
   float ksc, vsc;           // fp8 per-(block, head) scales (1 for bf16)
 };
 
-__device__ __forceinline__ uint32_t f32x2_hi_halves(float lo, float hi) {
-  // e4m3 values are exact in bf16: the top half of the fp32 pattern is the bf16.
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+// e4m3fn codes -> bf16, exact (every e4m3 value is a bf16 value), with the
+// hardware pair conversion v_cvt_scalef32_pk_bf16_fp8 at scale 1: bytes 0, 1
+// (word 0) or 2, 3 (word 1) of a dword become the low and high bf16 halves.
+template <bool WORD1>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, WORD1));
 }
 
 __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
   u32x4 r;
-  const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-  const floatx2 c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-  r[0] = f32x2_hi_halves(a[0], a[1]);
-  r[1] = f32x2_hi_halves(b[0], b[1]);
-  r[2] = f32x2_hi_halves(c[0], c[1]);
-  r[3] = f32x2_hi_halves(d[0], d[1]);
+  r[0] = fp8x2_to_bf16x2<false>(lo);
+  r[1] = fp8x2_to_bf16x2<true>(lo);
+  r[2] = fp8x2_to_bf16x2<false>(hi);
+  r[3] = fp8x2_to_bf16x2<true>(hi);
   return __builtin_bit_cast(bf16x8, r);
 }
 
 __device__ __forceinline__ shortx4 fp8x4_to_bf16x4(uint32_t w) {
-  const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
   u32x2 r;
-  r[0] = f32x2_hi_halves(a[0], a[1]);
-  r[1] = f32x2_hi_halves(b[0], b[1]);
+  r[0] = fp8x2_to_bf16x2<false>(w);
+  r[1] = fp8x2_to_bf16x2<true>(w);
   return __builtin_bit_cast(shortx4, r);
 }
 
