@@ -2,7 +2,7 @@
 
     python -m wavelet_amd.build
 
-One hipcc invocation compiles every ``csrc/*.hip`` source into
+hipcc compiles every ``csrc/*.hip`` source to an object and links them into
 ``wavelet_amd/libwkv.so``. The library links only the HIP runtime: no torch
 symbols cross the C ABI, so the same file is what a ctypes / cgo / JNI binding
 would load.
@@ -14,6 +14,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -26,7 +28,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # Code object v5: loadable by the HIP runtime torch bundles as well as /opt/rocm's.
     "-mcode-object-version=5",
     # Packed fp32 VALU ops are kept off for the whole device build.
@@ -36,6 +37,17 @@ HIPCC_FLAGS = [
     "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
+
+# Per-source additions.
+#   decode_gqa.hip: MFMA accumulators in ordinary VGPRs. Its online softmax
+#   rescales the output accumulators in place; with the accumulators in AGPRs
+#   the compiler copies all of them to VGPRs and back on every tile (64 moves
+#   per tile, measured in the ISA), whether or not a rescale happens. Its
+#   kernels need at most ~200 registers, so nothing is lost. (decode_mla.hip
+#   keeps AGPRs: its 1-wave-per-SIMD kernels use more than 256 registers.)
+EXTRA_FLAGS = {
+    "decode_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 
 
 def hipcc() -> str:
@@ -49,19 +61,34 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source into libwkv.so (always rebuilds)."""
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), *map(str, sources()), "-o", str(tmp)]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source (one object each, in parallel) and link libwkv.so (always rebuilds)."""
+    cc = hipcc()
+    inc = ["-I", str(PKG.parent / "include")]
+    with tempfile.TemporaryDirectory(prefix="wkv_build_") as tmpdir:
+        objs = []
+        cmds = []
+        for src in sources():
+            obj = Path(tmpdir) / (src.stem + ".o")
+            objs.append(obj)
+            cmds.append([cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *inc, "-c", str(src), "-o", str(obj)])
+        with ThreadPoolExecutor(max_workers=min(8, len(cmds))) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        tmp = LIB.with_suffix(".so.tmp")
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -74,6 +74,17 @@ __device__ __forceinline__ shortx4 fp8x4_to_bf16x4(uint32_t w) {
   return __builtin_bit_cast(shortx4, r);
 }
 
+// A pointer every lane holds the same value of, moved to scalar registers. A
+// buffer resource must be; when the compiler cannot prove it (it sometimes
+// computes a uniform address with vector instructions) it would otherwise
+// wrap every load in a loop over the distinct values.
+__device__ __forceinline__ const uint8_t *wave_uniform(const uint8_t *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint8_t *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Buffer-resource word 3 for raw (unformatted, unswizzled) buffers on gfx9-family parts.
 constexpr int kRawBufferWord3 = 0x00020000;
 
@@ -83,18 +94,20 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // offset per load, so no per-tile vector address arithmetic is needed.
 template <int D, bool FP8>
 __device__ __forceinline__ void load_tile(Tile<D, FP8> &t, const uint8_t *__restrict__ kc,
-                                          const uint8_t *__restrict__ vc, int64_t blk, int kvh, int Hkv, int BS,
+                                          const uint8_t *__restrict__ vc, int blk, int kvh, int Hkv, int BS,
                                           int o0, uint32_t koff, uint32_t voff) {
-  constexpr int X = FP8 ? 16 : 8;  // elements per 16-byte K chunk
-  constexpr int C = D / X;
   constexpr int ESZ = FP8 ? 1 : 2;
   const int region = D * BS * ESZ;  // bytes of one (block, head) region of K, and of V
-  const uint8_t *kb = kc + ((blk * Hkv + kvh) * C * BS + o0) * 16;
+  // Region index in 32 bits (the host keeps num_blocks * num_kv_heads below
+  // 2^31), in a scalar register, so the 64-bit address arithmetic stays scalar.
+  const int ridx = __builtin_amdgcn_readfirstlane(blk * Hkv + kvh);
+  const int64_t rbase = static_cast<int64_t>(ridx) * region;
+  const uint8_t *kb = wave_uniform(kc + rbase + o0 * 16);
   const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(kb), 0, region, kRawBufferWord3);
 #pragma unroll
   for (int j = 0; j < Tile<D, FP8>::NK; ++j)
     t.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kr, koff, j * 4 * BS * 16, 0);
-  const uint8_t *vb = vc + ((blk * Hkv + kvh) * D * BS + o0) * ESZ;
+  const uint8_t *vb = wave_uniform(vc + rbase + o0 * ESZ);
   const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(vb), 0, region, kRawBufferWord3);
 #pragma unroll
   for (int n = 0; n < Tile<D, FP8>::NPV; ++n) {
@@ -207,17 +220,15 @@ __device__ __forceinline__ void new_token_tile(Tile<D, false> &t, uint32_t nk, u
   }
 }
 
-// Attention of one wave over tokens [t_begin, t_end) of sequence b: returns
-// the unnormalised output, running max and this lane's share of the sum.
-// `my_blk` holds, in lane i, the id of the partition's i-th block (loaded by
-// the caller; the host keeps a partition within 64 blocks); each tile takes
-// its id with a register readlane.
-template <int D, bool FP8>
-__device__ __forceinline__ void attend_partition(DecodeState<D, FP8> &st, const uint8_t *__restrict__ kc,
-                                                 const uint8_t *__restrict__ vc, const float *__restrict__ ks,
-                                                 const float *__restrict__ vs, const bf16x8 *qop, int my_blk,
-                                                 int t_begin, int t_end, int kvh, int Hkv, int BS, int64_t NB,
-                                                 float scale_log2, int lane, int col, int grp) {
+// The tile loop of one wave over tokens [t_begin, t_end) of a block list:
+// `consume(tile)` attends each 16-token tile. `my_blk` holds, in lane i, the
+// id of the range's i-th block (loaded by the caller; the host keeps a range
+// within 64 blocks); each tile takes its id with a register readlane.
+template <int D, bool FP8, typename Consume>
+__device__ __forceinline__ void attend_range(Consume &&consume, const uint8_t *__restrict__ kc,
+                                             const uint8_t *__restrict__ vc, const float *__restrict__ ks,
+                                             const float *__restrict__ vs, int my_blk, int t_begin, int t_end,
+                                             int kvh, int Hkv, int BS, int64_t NB, int lane, int col, int grp) {
   if (t_end <= t_begin) return;
   const int n_tiles = (t_end - t_begin + 15) / 16;
   const int blk_first = t_begin / BS;
@@ -252,7 +263,6 @@ __device__ __forceinline__ void attend_partition(DecodeState<D, FP8> &st, const 
     if (blk < 0) blk = 0;
     load_tile<D, FP8>(t, kc, vc, blk, kvh, Hkv, BS, ts % BS, koff, voff);
   };
-  auto consume = [&](Tile<D, FP8> &t) { attend_tile<D, FP8>(st, t, qop, scale_log2, grp); };
   // The loop body is straight-line: tiles past the end are issued and attended
   // as fully masked (p = 0, V zeroed), which keeps the wait counts exact.
   Tile<D, FP8> t0, t1, t2;
@@ -266,6 +276,18 @@ __device__ __forceinline__ void attend_partition(DecodeState<D, FP8> &st, const 
     issue(t1, i + 4);
     consume(t2);
   }
+}
+
+// Attention of one wave over tokens [t_begin, t_end) of one sequence: returns
+// the unnormalised output, running max and this lane's share of the sum.
+template <int D, bool FP8>
+__device__ __forceinline__ void attend_partition(DecodeState<D, FP8> &st, const uint8_t *__restrict__ kc,
+                                                 const uint8_t *__restrict__ vc, const float *__restrict__ ks,
+                                                 const float *__restrict__ vs, const bf16x8 *qop, int my_blk,
+                                                 int t_begin, int t_end, int kvh, int Hkv, int BS, int64_t NB,
+                                                 float scale_log2, int lane, int col, int grp) {
+  attend_range<D, FP8>([&](Tile<D, FP8> &t) { attend_tile<D, FP8>(st, t, qop, scale_log2, grp); }, kc, vc, ks, vs,
+                       my_blk, t_begin, t_end, kvh, Hkv, BS, NB, lane, col, grp);
 }
 
 // Grid: (chunk, KV head, sequence); W waves per workgroup, wave w of chunk c
@@ -526,6 +548,7 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   const int G = num_q_heads / Hkv;
   if (G > 16) return fail(WKV_ERR_UNSUPPORTED, "query group size %d > 16 not supported", G);
   WKV_CHECK_ARG(Hkv <= 65535, "num_kv_heads too large");
+  WKV_CHECK_ARG(cache->num_blocks * Hkv <= INT32_MAX, "num_blocks * num_kv_heads must be below 2^31");
   WKV_CHECK_ARG(q != nullptr && aligned16(q), "q must be non-NULL and 16-byte aligned");
   WKV_CHECK_ARG(q_stride_b >= 0 && q_stride_h >= 0 && q_stride_b % 8 == 0 && q_stride_h % 8 == 0,
                 "q strides must be non-negative multiples of 8");
