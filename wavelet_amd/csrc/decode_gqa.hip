@@ -220,6 +220,19 @@ __device__ __forceinline__ void new_token_tile(Tile<D, false> &t, uint32_t nk, u
   }
 }
 
+// Tiles a wave keeps in registers: one being attended while the others load.
+// A wave's bytes in flight are what bound these kernels (HBM latency under load
+// is several microseconds), so the smaller tiles (fp8, head_dim 64) go deeper:
+//   bf16, d=128: 3 x 8 KB (the tile registers already limit the wave to 2 per SIMD)
+//   fp8 or d=64: DEPTH_SMALL x 4 KB
+#ifndef WKV_GQA_DEPTH_SMALL
+#define WKV_GQA_DEPTH_SMALL 3
+#endif
+template <int D, bool FP8>
+constexpr int pipeline_depth() {
+  return (D == 128 && !FP8) ? 3 : WKV_GQA_DEPTH_SMALL;
+}
+
 // The tile loop of one wave over tokens [t_begin, t_end) of a block list:
 // `consume(tile)` attends each 16-token tile. `my_blk` holds, in lane i, the
 // id of the range's i-th block (loaded by the caller; the host keeps a range
@@ -263,18 +276,26 @@ __device__ __forceinline__ void attend_range(Consume &&consume, const uint8_t *_
     if (blk < 0) blk = 0;
     load_tile<D, FP8>(t, kc, vc, blk, kvh, Hkv, BS, ts % BS, koff, voff);
   };
-  // The loop body is straight-line: tiles past the end are issued and attended
-  // as fully masked (p = 0, V zeroed), which keeps the wait counts exact.
-  Tile<D, FP8> t0, t1, t2;
-  issue(t0, 0);
-  issue(t1, 1);
-  for (int i = 0; i < n_tiles; i += 3) {
-    issue(t2, i + 2);
-    consume(t0);
-    issue(t0, i + 3);
-    consume(t1);
-    issue(t1, i + 4);
-    consume(t2);
+  // Loads are issued unconditionally, which keeps the wait counts exact; a
+  // tile past the end (or of an unmapped block) is skipped, uniformly, when its
+  // turn comes. NT tiles rotate; while tile i is attended, i+1 .. i+NT-1 load.
+  constexpr int NT = pipeline_depth<D, FP8>();
+  Tile<D, FP8> t[NT];
+  // The prologue's loads must go out in tile order: the wait before a tile
+  // counts the loads issued after it, and the loop-entry state is merged with
+  // the back edge's (the scheduler otherwise reorders these independent loads,
+  // which forces every loop iteration's first tile to wait for all but one).
+#pragma unroll
+  for (int k = 0; k < NT - 1; ++k) {
+    issue(t[k], k);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int i = 0; i < n_tiles; i += NT) {
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      issue(t[(k + NT - 1) % NT], i + k + NT - 1);
+      if (t[k].valid > 0) consume(t[k]);
+    }
   }
 }
 
