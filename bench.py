@@ -45,6 +45,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-reps", type=int, default=2, help="passes over all layers for per-launch timing")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--group-aware", action="store_true",
+                    help="qwen2.5-7b-groups: the group-aware decode (each shared prompt block read once per group) "
+                         "instead of decoding every member separately")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device to device (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -154,8 +157,9 @@ def cpu_baseline(args, hq, hkv, d, bs, scale, per_layer_bytes) -> dict:
     }
 
 
-def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0):
-    """Per-layer caches (own memory per layer), step buffers and a DecodeStep plan."""
+def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0, grouped: bool = False):
+    """Per-layer caches (own memory per layer), step buffers and a DecodeStep plan
+    (group-aware when `grouped`: the workload's groups share their prompt blocks)."""
     from wavelet_amd import PagedKVCache
     from wavelet_amd.plan import DecodeStep
 
@@ -185,8 +189,13 @@ def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0):
     bt = torch.from_numpy(w.block_tables).to(dev)
     sl = torch.from_numpy(w.context_lens).to(dev)
     slots = torch.from_numpy(w.new_token_slots()).to(dev)
+    group = {}
+    if grouped:
+        n_groups = w.batch // w.group_size
+        group = dict(group_size=w.group_size, max_prefix_len=w.prefix_len,
+                     prefix_lens=torch.full((n_groups,), w.prefix_len, dtype=torch.int32, device=dev))
     step = DecodeStep(caches, qs, ks, vs, outs, bt, sl, slots, w.scale, max_seq_len=int(w.context_lens.max()),
-                      partition_size=args.partition)
+                      partition_size=args.partition, **group)
     return step, caches[0].nbytes
 
 
@@ -211,9 +220,12 @@ def workload(args, torch, dev) -> dict:
     elif name == "qwen2.5-7b-groups":
         w = synth.qwen25_7b_group_workload()
         args.layers = args.layers or 28
-        step, cache_bytes = _gqa_setup(torch, dev, args, w, "fp8_e4m3")
+        grouped = bool(getattr(args, "group_aware", False))
+        step, cache_bytes = _gqa_setup(torch, dev, args, w, "fp8_e4m3", grouped=grouped)
         kv_bytes = 1
-        desc = "Qwen2.5-7B GRPO groups, fp8 KV: 28 layers x (fp8 append + GQA decode), 32 x 8 seqs, shared 1024-token prompts"
+        desc = ("Qwen2.5-7B GRPO groups, fp8 KV: 28 layers x (fp8 append + GQA decode), 32 x 8 seqs, shared "
+                "1024-token prompts" + (" (group-aware: each prompt block read once per group)" if grouped else
+                                        " (members decoded separately)"))
     elif name == "deepseek-v3-mla":
         w = synth.deepseek_v3_mla_workload()
         args.layers = args.layers or 8
@@ -255,7 +267,9 @@ def workload(args, torch, dev) -> dict:
     attn = kv_unique + scales + B * HQ * D * 2 * 2 + int(((L + BS - 1) // BS).sum()) * 4 + B * 4
     append = B * 2 * HKV * D * (2 + kv_bytes) + B * 8
     return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
-            "kernel": f"decode_gqa_kernel<{D},{'true' if kv_bytes == 1 else 'false'},true,W>",
+            "kernel": (f"decode_gqa_grouped_kernel<{D},true,true,4> (+ decode_grouped_merge_kernel)"
+                       if getattr(step, "grouped", False) else
+                       f"decode_gqa_kernel<{D},{'true' if kv_bytes == 1 else 'false'},true,W>"),
             "dtype": "fp8_e4m3 KV, bf16 q/o" if kv_bytes == 1 else "bf16", "desc": desc,
             "flops_per_layer": 4 * int(L.sum()) * HQ * D, "cache_bytes": cache_bytes,
             "logical_kv_bytes": int(L.sum()) * 2 * HKV * D * kv_bytes}

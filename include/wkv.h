@@ -170,6 +170,36 @@ int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64
                                 const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
                                 int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Group-aware decode for GRPO groups (the n samples of one prompt):
+ * sequences g*group_size .. g*group_size+group_size-1 form group g (the last
+ * group may be short), and the first prefix_lens[g] tokens of every member are
+ * stored in the same physical blocks -- identical block-table entries, as
+ * SamplingParams(n=num_generations) leaves them (engine.py:69-90) and
+ * BlockManager.share_prefix builds them. The shared prompt blocks are read
+ * once per (group, KV head) for all the group's query rows instead of once per
+ * member (a plain decode re-reads them group_size times); each member's own
+ * tokens are attended as in wkv_paged_decode_gqa, and the parts are merged by
+ * log-sum-exp. The result equals wkv_paged_decode_gqa (or, with key, value and
+ * slot_mapping given, wkv_append_paged_decode_gqa) on the same inputs, to
+ * floating-point reassociation. key, value and slot_mapping are all NULL for
+ * attention only. The kernel cuts each group's prefix to whole blocks held by
+ * every member (and before a token this call appends); max_prefix_len bounds
+ * prefix_lens. workspace: wkv_grouped_decode_workspace_size() bytes. No
+ * reference counterpart computes this (vLLM decodes each member separately);
+ * the group semantics are the reference's (engine.py:69-90, :1034-1038). */
+int64_t wkv_grouped_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim,
+                                          int32_t max_seq_len, int32_t max_prefix_len, int32_t partition_size);
+
+int wkv_paged_decode_gqa_grouped(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                 int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                 int64_t value_stride_h, const int64_t *slot_mapping, const void *q,
+                                 int64_t q_stride_b, int64_t q_stride_h, void *out, int32_t num_q_heads,
+                                 const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                 const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
+                                 const int32_t *prefix_lens, int32_t group_size, int32_t max_prefix_len,
+                                 float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
+                                 void *stream);
+
 /* Weight-absorbed MLA decode over the latent cache:
  *   s = (q_nope . c_kv + q_pe . k_pe) * scale; o = softmax(s) . c_kv
  * q_nope [batch, num_heads, kv_lora_rank], q_pe [batch, num_heads, rope_dim]

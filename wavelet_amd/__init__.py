@@ -5,11 +5,13 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
 * ``PagedKVCache`` / ``MLALatentCache`` -- per-layer caches with ``append``,
   ``gather`` and ``copy_blocks``;
 * ``paged_decode_gqa`` / ``paged_decode_mla`` -- one decode step of attention;
+* ``paged_decode_gqa_grouped`` -- the same for GRPO groups, reading each
+  group's shared prompt blocks once;
 * ``BlockManager`` -- host-side block allocation with ref-counted prefix
   sharing for GRPO groups.
 """
 
-from .attention import paged_decode_gqa, paged_decode_mla
+from .attention import paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla
 from .blocks import BlockManager
 from .cache import MLALatentCache, PagedKVCache, validate_tables
 
@@ -18,6 +20,7 @@ __all__ = [
     "MLALatentCache",
     "PagedKVCache",
     "paged_decode_gqa",
+    "paged_decode_gqa_grouped",
     "paged_decode_mla",
     "validate_tables",
 ]

@@ -118,6 +118,90 @@ def paged_decode_gqa(
     return out
 
 
+def paged_decode_gqa_grouped(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    prefix_lens: torch.Tensor,
+    group_size: int,
+    scale: float,
+    *,
+    max_seq_len: int | None = None,
+    max_prefix_len: int | None = None,
+    out: torch.Tensor | None = None,
+    partition_size: int = 0,
+    new_key: torch.Tensor | None = None,
+    new_value: torch.Tensor | None = None,
+    slot_mapping: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``paged_decode_gqa`` for GRPO groups that read their shared prompt once.
+
+    Sequences ``g*group_size .. g*group_size+group_size-1`` form group ``g``;
+    ``prefix_lens [n_groups]`` int32 gives the leading tokens whose physical
+    blocks every member's table shares (``BlockManager.shared_prefix_tokens``).
+    The result equals ``paged_decode_gqa`` on the same inputs (to fp32
+    reassociation); the shared blocks are streamed once per group and KV head
+    for all of the group's query rows. Optional fused append as in
+    ``paged_decode_gqa`` (the group semantics follow ``SamplingParams(n=...)``,
+    wavelet/inference/engine.py:69-90).
+    """
+    if not isinstance(cache, PagedKVCache):
+        raise ValueError("cache must be a PagedKVCache")
+    dev = cache.device
+    block_table, seq_lens = check_tables(block_table, seq_lens, dev, cache.block_size)
+    batch = seq_lens.shape[0]
+    group_size = int(group_size)
+    if group_size < 1 or (batch and group_size > batch):
+        raise ValueError(f"group_size must be in [1, batch={batch}] (got {group_size})")
+    n_groups = -(-batch // group_size) if batch else 0
+    _require_cuda(prefix_lens, "prefix_lens", dev)
+    if prefix_lens.dtype != torch.int32 or prefix_lens.dim() != 1 or prefix_lens.shape[0] != n_groups:
+        raise ValueError(f"prefix_lens must be int32 [{n_groups}] (got {prefix_lens.dtype} {tuple(prefix_lens.shape)})")
+    prefix_lens = prefix_lens.contiguous()
+    if q.dim() != 3 or q.shape[0] != batch:
+        raise ValueError(f"q must be [B={batch}, Hq, D]")
+    hq = q.shape[1]
+    q = _query(q, "q", (hq, cache.head_dim), dev)
+    fused = new_key is not None or new_value is not None or slot_mapping is not None
+    if fused:
+        if new_key is None or new_value is None or slot_mapping is None:
+            raise ValueError("a fused append needs new_key, new_value and slot_mapping together")
+        shape = (cache.num_kv_heads, cache.head_dim)
+        new_key = _token_rows(new_key, "new_key", shape, dev)
+        new_value = _token_rows(new_value, "new_value", shape, dev)
+        if new_key.shape[0] != batch or new_value.shape[0] != batch:
+            raise ValueError(f"new_key/new_value must hold one token per sequence ({batch})")
+        slot_mapping = _slots(slot_mapping, batch, dev)
+    if out is None:
+        out = torch.empty((batch, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, hq, cache.head_dim) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 [B, Hq, D] tensor")
+    if batch == 0:
+        return out
+    lib = _lib.load()
+    msl = _max_len(seq_lens, max_seq_len)
+    mpl = int(max_prefix_len) if max_prefix_len is not None else (
+        int(prefix_lens.max().item()) if prefix_lens.numel() else 0)
+    need = lib.wkv_grouped_decode_workspace_size(batch, hq, cache.head_dim, max(msl, 1), max(mpl, 0),
+                                                 int(partition_size))
+    if need < 0:
+        raise ValueError("invalid grouped decode geometry")
+    ws = _workspace(dev, need)
+    if fused:
+        head = (new_key.data_ptr(), new_key.stride(0), new_key.stride(1), new_value.data_ptr(), new_value.stride(0),
+                new_value.stride(1), slot_mapping.data_ptr())
+    else:
+        head = (None, 0, 0, None, 0, 0, None)
+    rc = lib.wkv_paged_decode_gqa_grouped(
+        ctypes.byref(cache.descriptor()), *head, q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl,
+        prefix_lens.data_ptr(), group_size, mpl, float(scale), int(partition_size), ws.data_ptr(), ws.numel(),
+        _stream(dev))
+    _lib.check(rc, "paged_decode_gqa_grouped")
+    return out
+
+
 def paged_decode_mla(
     q_nope: torch.Tensor,
     q_pe: torch.Tensor,

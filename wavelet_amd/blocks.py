@@ -217,6 +217,19 @@ class BlockManager:
     def ref_count(self, block: int) -> int:
         return int(self._ref[block])
 
+    def shared_prefix_tokens(self, seq_ids) -> int:
+        """Leading tokens every sequence in ``seq_ids`` reads from the same physical
+        blocks: the ``prefix_lens`` entry of a group for ``paged_decode_gqa_grouped``
+        (a GRPO group after ``share_prefix`` / ``fork``, engine.py:69-90)."""
+        seqs = [self._seqs[s] for s in seq_ids]
+        if not seqs:
+            return 0
+        n = min(len(s.blocks) for s in seqs)
+        shared = 0
+        while shared < n and all(s.blocks[shared] == seqs[0].blocks[shared] for s in seqs[1:]):
+            shared += 1
+        return min(shared * self.block_size, min(s.length for s in seqs))
+
     def tables(self, seq_ids, width: int | None = None) -> tuple[np.ndarray, np.ndarray]:
         """``block_table [B, width]`` int32 (unused entries -1) and ``seq_lens [B]`` int32."""
         seqs = [self._seqs[s] for s in seq_ids]

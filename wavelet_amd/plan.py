@@ -37,12 +37,18 @@ class DecodeStep:
     step buffers; ``block_table`` / ``seq_lens`` / ``slot_mapping`` are shared by
     all layers (as in a paged engine, one table per sequence). ``slot_mapping[b]``
     is the slot of sequence ``b``'s new token (one token per sequence).
+
+    With ``group_size`` and ``prefix_lens`` (int32 ``[n_groups]`` on the device)
+    the attention is the group-aware one (``paged_decode_gqa_grouped``): GRPO
+    groups of ``group_size`` consecutive sequences read their shared prompt
+    blocks once per group; ``max_prefix_len`` bounds ``prefix_lens``.
     """
 
     def __init__(self, caches: list[PagedKVCache], q: list[torch.Tensor], key: list[torch.Tensor],
                  value: list[torch.Tensor], out: list[torch.Tensor], block_table: torch.Tensor,
                  seq_lens: torch.Tensor, slot_mapping: torch.Tensor, scale: float, max_seq_len: int,
-                 partition_size: int = 0) -> None:
+                 partition_size: int = 0, *, group_size: int = 0, prefix_lens: torch.Tensor | None = None,
+                 max_prefix_len: int = 0) -> None:
         if not caches:
             raise ValueError("no layers")
         dev = caches[0].device
@@ -54,7 +60,17 @@ class DecodeStep:
         batch = self.seq_lens.shape[0]
         lib = _lib.load()
         hq = q[0].shape[1]
-        need = lib.wkv_decode_workspace_size(batch, hq, c0.head_dim, max_seq_len, int(partition_size))
+        self.grouped = group_size > 0
+        if self.grouped:
+            n_groups = -(-batch // group_size)
+            if (prefix_lens is None or prefix_lens.dtype != torch.int32 or tuple(prefix_lens.shape) != (n_groups,)
+                    or not prefix_lens.is_contiguous() or prefix_lens.device != dev):
+                raise ValueError(f"prefix_lens must be a contiguous int32 [{n_groups}] tensor on {dev}")
+            self.prefix_lens = prefix_lens
+            need = lib.wkv_grouped_decode_workspace_size(batch, hq, c0.head_dim, max_seq_len, int(max_prefix_len),
+                                                         int(partition_size))
+        else:
+            need = lib.wkv_decode_workspace_size(batch, hq, c0.head_dim, max_seq_len, int(partition_size))
         if need < 0:
             raise ValueError("invalid decode geometry")
         self.workspace = _workspace(dev, need)
@@ -76,9 +92,15 @@ class DecodeStep:
                     self.block_table.data_ptr(), self.block_table.stride(0), self.block_table.shape[1],
                     self.seq_lens.data_ptr(), batch, int(max_seq_len), ctypes.c_float(scale),
                     int(partition_size), self.workspace.data_ptr(), self.workspace.numel(), self.stream)
-            decode_args = (desc, *tail)
-            fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
-                          vv.stride(1), slot_mapping.data_ptr(), *tail)
+            if self.grouped:
+                gtail = (*tail[:11], self.prefix_lens.data_ptr(), int(group_size), int(max_prefix_len), *tail[11:])
+                decode_args = (desc, None, 0, 0, None, 0, 0, None, *gtail)
+                fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
+                              vv.stride(1), slot_mapping.data_ptr(), *gtail)
+            else:
+                decode_args = (desc, *tail)
+                fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
+                              vv.stride(1), slot_mapping.data_ptr(), *tail)
             self.calls.append(_LayerCall(fn, append_args, decode_args, fused_args))
         self._keep = (caches, q, key, value, out)
 
@@ -89,13 +111,15 @@ class DecodeStep:
             _lib.check(rc, f"append layer {layer}")
 
     def attend(self, layer: int) -> None:
-        rc = self.lib.wkv_paged_decode_gqa(*self.calls[layer].decode_args)
+        fn = self.lib.wkv_paged_decode_gqa_grouped if self.grouped else self.lib.wkv_paged_decode_gqa
+        rc = fn(*self.calls[layer].decode_args)
         if rc:
             _lib.check(rc, f"decode layer {layer}")
 
     def step_layer(self, layer: int) -> None:
         """Append + attention of one layer in a single launch (plus the partition merge)."""
-        rc = self.lib.wkv_append_paged_decode_gqa(*self.calls[layer].fused_args)
+        fn = self.lib.wkv_paged_decode_gqa_grouped if self.grouped else self.lib.wkv_append_paged_decode_gqa
+        rc = fn(*self.calls[layer].fused_args)
         if rc:
             _lib.check(rc, f"append+decode layer {layer}")
 
