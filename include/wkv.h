@@ -200,6 +200,27 @@ int wkv_paged_decode_gqa_grouped(const wkv_cache_t *cache, const void *key, int6
                                  float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
                                  void *stream);
 
+/* Varlen GQA prefill / chunked prefill over the paged cache. Sequence b
+ * brings n_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] new tokens (rows of q
+ * [num_tokens, num_q_heads, head_dim] and out, bf16, last dim contiguous) at
+ * positions seq_lens[b] - n_b .. seq_lens[b] - 1; new token j attends to
+ * positions 0 .. seq_lens[b] - n_b + j (causal, aligned to the end of the
+ * context: cached context -- an earlier chunk or a prefix-cache hit -- is
+ * attended in full). With key/value/slot_mapping given (num_tokens rows) the
+ * new tokens are first appended exactly as wkv_append / wkv_append_fp8 would,
+ * then attended from the cache; with all three NULL the cache must already
+ * hold them. max_query_len >= every n_b; no workspace.
+ * Replaces the prompt step of llm.generate (engine.py:887): vLLM's
+ * reshape_and_cache followed by its varlen flash-attention over the paged
+ * cache (the prefix-cache path reads cached blocks, engine.py:1034-1038). */
+int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
+                    const void *value, int64_t value_stride_t, int64_t value_stride_h, const int64_t *slot_mapping,
+                    int64_t num_tokens, const void *q, int64_t q_stride_t, int64_t q_stride_h, void *out,
+                    int64_t out_stride_t, int64_t out_stride_h, int32_t num_q_heads, const int32_t *cu_seqlens_q,
+                    const int32_t *seq_lens, const int32_t *block_table, int64_t bt_stride,
+                    int32_t max_blocks_per_seq, int32_t batch, int32_t max_query_len, int32_t max_seq_len,
+                    float scale, void *stream);
+
 /* Weight-absorbed MLA decode over the latent cache:
  *   s = (q_nope . c_kv + q_pe . k_pe) * scale; o = softmax(s) . c_kv
  * q_nope [batch, num_heads, kv_lora_rank], q_pe [batch, num_heads, rope_dim]

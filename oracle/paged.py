@@ -237,6 +237,46 @@ def decode_gqa(q, k_vals, v_vals, block_table, seq_lens, scale, *, p_bf16=False,
     return out
 
 
+def prefill_gqa(q, k_vals, v_vals, block_table, seq_lens, cu_seqlens_q, scale, *, p_bf16=False, dtype=np.float64):
+    """Varlen GQA prefill over a paged context (chunked prefill).
+
+    Sequence ``i`` brings ``n_i = cu_seqlens_q[i+1] - cu_seqlens_q[i]`` new
+    tokens, rows ``cu_seqlens_q[i] ..`` of ``q`` ``[T, Hq, D]``, at positions
+    ``L_i - n_i .. L_i - 1`` (``L_i = seq_lens[i]`` counts the cached context
+    and the new tokens, whose K/V are already in the cache). New token ``j``
+    attends to positions ``0 .. L_i - n_i + j``: the causal mask of the
+    engine's prompt step (``llm.generate``, wavelet/inference/engine.py:887)
+    aligned to the end of the context, so an earlier chunk or a prefix-cache
+    hit is simply cached context. Scores and softmax as in ``decode_gqa``.
+    Returns ``[T, Hq, D]`` in ``dtype``.
+    """
+    q = np.asarray(q)
+    t, hq, d = q.shape
+    nb, bs, hkv, _ = k_vals.shape
+    g = hq // hkv
+    out = np.zeros((t, hq, d), dtype=dtype)
+    for i in range(len(seq_lens)):
+        q0, q1 = int(cu_seqlens_q[i]), int(cu_seqlens_q[i + 1])
+        n, length = q1 - q0, int(seq_lens[i])
+        if n == 0 or length == 0:
+            continue
+        pos = np.arange(length)
+        blk = np.asarray(block_table[i], dtype=np.int64)[pos // bs]
+        kk = k_vals[blk, pos % bs].astype(dtype)  # [L, Hkv, D]
+        vv = v_vals[blk, pos % bs].astype(dtype)
+        qpos = length - n + np.arange(n)  # [n]
+        mask = pos[None, :] <= qpos[:, None]  # [n, L]
+        for h in range(hkv):
+            for hh in range(h * g, (h + 1) * g):
+                s = (q[q0:q1, hh].astype(dtype) @ kk[:, h].T) * dtype(scale)  # [n, L]
+                s = np.where(mask, s, -np.inf)
+                p = _softmax_rows(s)
+                if p_bf16:
+                    p = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(dtype)
+                out[q0:q1, hh] = p @ vv[:, h]
+    return out
+
+
 def decode_mla(q, latent_vals, block_table, seq_lens, scale, kv_lora_rank=512, *, p_bf16=False, dtype=np.float64):
     """Weight-absorbed MLA decode over a single latent head.
 

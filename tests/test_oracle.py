@@ -396,3 +396,47 @@ def test_decode_zero_length_gives_zeros():
     kc = np.zeros((1, 16, 1, 64), np.float32)
     out = paged.decode_gqa(np.ones((1, 2, 64)), kc, kc, np.array([[0]]), np.array([0]), 0.125)
     assert np.all(out == 0)
+
+
+def _prefill_case(name, hq, hkv, d, bs, qlens, lens):
+    w = synth.make_decode_workload(name, batch=len(lens), num_kv_heads=hkv, num_q_heads=hq, head_dim=d,
+                                   block_size=bs, context_lens=np.asarray(lens))
+    kv, vv = _random_cache_values(w, "p")
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int64)
+    q = paged.bf16_to_f32(synth.normal_bf16(synth.stream_key(name, "q"), (int(cu[-1]), hq, d)))
+    return w, kv, vv, cu, q
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128)])
+def test_prefill_gqa_matches_torch_sdpa_with_explicit_mask(hq, hkv, d):
+    """Against torch's scaled_dot_product_attention (float64) with the end-aligned causal mask."""
+    qlens, lens = [5, 16, 1, 33], [5, 40, 300, 33]  # whole prompt, chunk after context, decode-like, one block+
+    w, kv, vv, cu, q = _prefill_case(f"pf{hq}", hq, hkv, d, 16, qlens, lens)
+    got = paged.prefill_gqa(q, kv, vv, w.block_tables, w.context_lens, cu, w.scale)
+    g = hq // hkv
+    for i, (n, length) in enumerate(zip(qlens, lens)):
+        pos = np.arange(length)
+        blk = w.block_tables[i][pos // 16]
+        kk = torch.from_numpy(kv[blk, pos % 16].astype(np.float64)).permute(1, 0, 2).repeat_interleave(g, 0)
+        vv_ = torch.from_numpy(vv[blk, pos % 16].astype(np.float64)).permute(1, 0, 2).repeat_interleave(g, 0)
+        qq = torch.from_numpy(q[cu[i]:cu[i + 1]].astype(np.float64)).permute(1, 0, 2)  # [Hq, n, D]
+        mask = torch.from_numpy(pos[None, :] <= (length - n + np.arange(n))[:, None])
+        o = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv_, attn_mask=mask, scale=w.scale)
+        np.testing.assert_allclose(got[cu[i]:cu[i + 1]], o.permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_prefill_gqa_consistent_with_decode_and_closed_forms():
+    qlens, lens = [7, 1, 20], [7, 50, 64]
+    w, kv, vv, cu, q = _prefill_case("pfc", 8, 2, 64, 16, qlens, lens)
+    got = paged.prefill_gqa(q, kv, vv, w.block_tables, w.context_lens, cu, w.scale)
+    # the last new token of every sequence sees the whole context: decode over L
+    last = q[cu[1:] - 1]
+    dec = paged.decode_gqa(last, kv, vv, w.block_tables, w.context_lens, w.scale)
+    np.testing.assert_allclose(got[cu[1:] - 1], dec, rtol=1e-12, atol=1e-13)
+    # the first token of a prompt with no context attends only to itself: o = v_0 exactly
+    v0 = vv[w.block_tables[0][0], 0]  # [Hkv, D]
+    np.testing.assert_array_equal(got[0], np.repeat(v0, 4, axis=0))
+    # a new token j of sequence 2 (context 44) equals decode over its first 44 + j + 1 positions
+    j = 9
+    dec_j = paged.decode_gqa(q[cu[2] + j][None], kv, vv, w.block_tables[2:3], np.array([44 + j + 1]), w.scale)
+    np.testing.assert_allclose(got[cu[2] + j], dec_j[0], rtol=1e-12, atol=1e-13)

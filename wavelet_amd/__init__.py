@@ -7,11 +7,13 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
 * ``paged_decode_gqa`` / ``paged_decode_mla`` -- one decode step of attention;
 * ``paged_decode_gqa_grouped`` -- the same for GRPO groups, reading each
   group's shared prompt blocks once;
+* ``prefill_gqa`` -- varlen (chunked) prefill that appends the prompt's K/V
+  and attends causally over the paged context;
 * ``BlockManager`` -- host-side block allocation with ref-counted prefix
   sharing for GRPO groups.
 """
 
-from .attention import paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla
+from .attention import paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla, prefill_gqa
 from .blocks import BlockManager
 from .cache import MLALatentCache, PagedKVCache, validate_tables
 
@@ -22,5 +24,6 @@ __all__ = [
     "paged_decode_gqa",
     "paged_decode_gqa_grouped",
     "paged_decode_mla",
+    "prefill_gqa",
     "validate_tables",
 ]

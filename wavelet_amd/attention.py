@@ -202,6 +202,77 @@ def paged_decode_gqa_grouped(
     return out
 
 
+def prefill_gqa(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    scale: float,
+    *,
+    key: torch.Tensor | None = None,
+    value: torch.Tensor | None = None,
+    slot_mapping: torch.Tensor | None = None,
+    max_query_len: int | None = None,
+    max_seq_len: int | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Varlen (chunked) prefill: ``q [T, Hq, D]`` bf16 -> ``[T, Hq, D]`` bf16.
+
+    Sequence ``b`` owns rows ``cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1`` (int32
+    ``[B+1]``), new tokens at positions ``seq_lens[b] - n_b ..`` of a context
+    of ``seq_lens[b]`` tokens (earlier chunks / prefix-cache hits are cached
+    context); token ``j`` attends causally to positions ``0 .. seq_lens[b] -
+    n_b + j``. With ``key``/``value`` ``[T, Hkv, D]`` and ``slot_mapping [T]``
+    the new tokens are appended first (``cache.append``) and attended from the
+    cache -- the prompt step of ``llm.generate`` (wavelet/inference/
+    engine.py:887). ``max_query_len`` / ``max_seq_len`` (host ints) avoid
+    device syncs when given.
+    """
+    if not isinstance(cache, PagedKVCache):
+        raise ValueError("cache must be a PagedKVCache")
+    dev = cache.device
+    block_table, seq_lens = check_tables(block_table, seq_lens, dev, cache.block_size)
+    batch = seq_lens.shape[0]
+    _require_cuda(cu_seqlens_q, "cu_seqlens_q", dev)
+    if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_q.dim() != 1 or cu_seqlens_q.shape[0] != batch + 1:
+        raise ValueError(f"cu_seqlens_q must be int32 [{batch + 1}]")
+    cu_seqlens_q = cu_seqlens_q.contiguous()
+    if q.dim() != 3:
+        raise ValueError("q must be [T, Hq, D]")
+    tokens, hq = q.shape[0], q.shape[1]
+    q = _query(q, "q", (hq, cache.head_dim), dev)
+    append = key is not None or value is not None or slot_mapping is not None
+    if append:
+        if key is None or value is None or slot_mapping is None:
+            raise ValueError("appending needs key, value and slot_mapping together")
+        shape = (cache.num_kv_heads, cache.head_dim)
+        key = _token_rows(key, "key", shape, dev)
+        value = _token_rows(value, "value", shape, dev)
+        if key.shape[0] != tokens or value.shape[0] != tokens:
+            raise ValueError(f"key/value must hold the {tokens} new tokens")
+        slot_mapping = _slots(slot_mapping, tokens, dev)
+    if out is None:
+        out = torch.empty((tokens, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (tokens, hq, cache.head_dim) or out.stride(2) != 1:
+        raise ValueError("out must be a bfloat16 [T, Hq, D] tensor with a contiguous last dim")
+    if max_query_len is None:
+        max_query_len = int((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max().item()) if batch else 0
+    msl = _max_len(seq_lens, max_seq_len)
+    lib = _lib.load()
+    if append:
+        head = (key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0), value.stride(1),
+                slot_mapping.data_ptr(), tokens)
+    else:
+        head = (None, 0, 0, None, 0, 0, None, 0)
+    rc = lib.wkv_prefill_gqa(
+        ctypes.byref(cache.descriptor()), *head, q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(),
+        out.stride(0), out.stride(1), hq, cu_seqlens_q.data_ptr(), seq_lens.data_ptr(), block_table.data_ptr(),
+        block_table.stride(0), block_table.shape[1], batch, int(max_query_len), msl, float(scale), _stream(dev))
+    _lib.check(rc, "prefill_gqa")
+    return out
+
+
 def paged_decode_mla(
     q_nope: torch.Tensor,
     q_pe: torch.Tensor,

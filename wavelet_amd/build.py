@@ -39,7 +39,7 @@ HIPCC_FLAGS = [
 ]
 
 # Per-source additions.
-#   decode_gqa.hip: MFMA accumulators in ordinary VGPRs. Its online softmax
+#   decode_gqa.hip, prefill_gqa.hip: MFMA accumulators in ordinary VGPRs. Its online softmax
 #   rescales the output accumulators in place; with the accumulators in AGPRs
 #   the compiler copies all of them to VGPRs and back on every tile (64 moves
 #   per tile, measured in the ISA), whether or not a rescale happens. Its
@@ -47,6 +47,7 @@ HIPCC_FLAGS = [
 #   keeps AGPRs: its 1-wave-per-SIMD kernels use more than 256 registers.)
 EXTRA_FLAGS = {
     "decode_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "prefill_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],  # the same tile code
 }
 
 
