@@ -28,6 +28,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
 
 
 def parse() -> argparse.Namespace:
@@ -36,7 +37,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="qwen3-4b",
-                    choices=["qwen3-4b", "qwen3-4b-var", "qwen2.5-0.5b", "qwen2.5-7b-groups", "deepseek-v3-mla"],
+                    choices=["qwen3-4b", "qwen3-4b-var", "qwen2.5-0.5b", "qwen2.5-7b-groups", "deepseek-v3-mla",
+                             "qwen3-4b-prefill"],
                     help="qwen3-4b is the headline; the others are the remaining measured shapes")
     ap.add_argument("--layers", type=int, default=0, help="0 = the model's depth (8 rotated layers for MLA)")
     ap.add_argument("--batch", type=int, default=64)
@@ -255,6 +257,40 @@ def workload(args, torch, dev) -> dict:
                 "cache_bytes": cache_bytes,
                 "desc": f"DeepSeek-V3 MLA decode: {args.layers} layers x (latent append + absorbed attention), "
                         "128 heads, 512+64 latent, B=32, context 4096, block 64"}
+    elif name == "qwen3-4b-prefill":
+        # the prompt step: 8 prompts of 2,048 tokens, no cached context
+        from wavelet_amd import PagedKVCache
+        from wavelet_amd.plan import PrefillStep
+
+        n_new, B = 2048, 8
+        w = synth.make_decode_workload(name, batch=B, num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16,
+                                       context_lens=np.full(B, n_new))
+        args.layers = args.layers or 36
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1234)
+        T, HQ, HKV, D, BS = B * n_new, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
+        caches, qs, ks, vs, outs = [], [], [], [], []
+        for _ in range(args.layers):
+            caches.append(PagedKVCache(w.num_blocks, BS, HKV, D, device=dev))
+            qs.append(torch.randn((T, HQ, D), generator=gen, device=dev).to(torch.bfloat16))
+            ks.append(torch.randn((T, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
+            vs.append(torch.randn((T, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
+            outs.append(torch.empty((T, HQ, D), dtype=torch.bfloat16, device=dev))
+        pos = np.arange(n_new)
+        slots = np.concatenate([w.block_tables[i][pos // BS].astype(np.int64) * BS + pos % BS for i in range(B)])
+        cu = torch.arange(0, T + 1, n_new, dtype=torch.int32, device=dev)
+        step = PrefillStep(caches, qs, ks, vs, outs, torch.from_numpy(w.block_tables).to(dev),
+                           torch.from_numpy(w.context_lens).to(dev), cu, torch.from_numpy(slots).to(dev), w.scale,
+                           max_query_len=n_new, max_seq_len=n_new)
+        visible = B * n_new * (n_new + 1) // 2  # (query, key) pairs under the causal mask
+        flops = 4 * visible * HQ * D
+        append = T * 2 * HKV * D * (2 + 2) + T * 8
+        attn = T * HQ * D * 2 * 2 + T * 2 * HKV * D * 2  # q in, o out, the prompt's K/V read once
+        return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
+                "kernel": "prefill_gqa_kernel<128,false> (+ append_bf16_kernel)", "dtype": "bf16",
+                "flops_per_layer": flops, "cache_bytes": caches[0].nbytes, "bound": "mfma",
+                "desc": f"Qwen3-4B prompt step: {args.layers} layers x (append + causal prefill attention), "
+                        f"{B} prompts x {n_new} tokens, 32 q / 8 kv heads, d=128, bf16, block 16"}
     else:
         raise SystemExit(f"unknown workload {name}")
     L = w.context_lens.astype(np.int64)
@@ -333,6 +369,27 @@ def main() -> int:
     achieved = wl["layer_bytes"] / (kernel_us * 1e-6) / 1e9
     headline = wl["name"] == "qwen3-4b"
     B = w.batch
+    if wl.get("bound") == "mfma":  # compute-bound workload: TFLOP/s against the dense bf16 MFMA peak
+        tflops_step = wl["flops_per_layer"] * args.layers / (ms_per_step * 1e-3) / 1e12
+        tflops_launch = wl["flops_per_layer"] / (kernel_us * 1e-6) / 1e12
+        rec = {
+            "metric": f"prefill attention TFLOP/s & us/step, {wl['name']}",
+            "value": round(tflops_step, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "us_per_step": round(ms_per_step * 1e3, 1),
+            "mfma_frac": round(tflops_step / MFMA_PEAK_BF16_TFLOPS, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": wl["dtype"],
+            "data": "synthetic (random q/K/V, seeded), resident in HBM",
+            "config": {"workload": wl["desc"], "layers": args.layers, "batch": B,
+                       "q_heads": w.num_q_heads, "kv_heads": w.num_kv_heads, "head_dim": w.head_dim,
+                       "block_size": w.block_size, "flops_per_step": wl["flops_per_layer"] * args.layers},
+            "roofline": {"bound": "mfma", "kernel": wl["kernel"], "achieved": round(tflops_launch, 1),
+                         "peak": MFMA_PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops_launch / MFMA_PEAK_BF16_TFLOPS, 4), "traffic": None,
+                         "mean_launch_us": round(kernel_us, 2), "hbm_gbs": round(achieved, 1)},
+            "unfused_us": {"append": round(append_us, 2), "attention": round(attend_us, 2)},
+        }
+        print(json.dumps(rec), flush=True)
+        return 0
     rec = {
         "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx" if headline
         else f"decode-attn+KV-append GB/s & us/step, {wl['name']}",

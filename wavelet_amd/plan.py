@@ -196,3 +196,72 @@ class MLADecodeStep:
     def run(self) -> None:
         for layer in range(len(self.calls)):
             self.step_layer(layer)
+
+
+class PrefillStep:
+    """Pre-validated prompt step for every layer: append the new tokens' K/V and
+    attend causally over each sequence's paged context (``prefill_gqa``).
+
+    ``q[l]`` ``[T, Hq, D]``, ``key[l]`` / ``value[l]`` ``[T, Hkv, D]`` and
+    ``out[l]`` are layer ``l``'s buffers; ``cu_seqlens_q [B+1]`` int32 splits
+    the ``T`` rows by sequence and ``slot_mapping [T]`` places them.
+    """
+
+    def __init__(self, caches: list[PagedKVCache], q: list[torch.Tensor], key: list[torch.Tensor],
+                 value: list[torch.Tensor], out: list[torch.Tensor], block_table: torch.Tensor,
+                 seq_lens: torch.Tensor, cu_seqlens_q: torch.Tensor, slot_mapping: torch.Tensor, scale: float,
+                 max_query_len: int, max_seq_len: int) -> None:
+        if not caches:
+            raise ValueError("no layers")
+        dev = caches[0].device
+        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, caches[0].block_size)
+        batch = self.seq_lens.shape[0]
+        if (cu_seqlens_q.dtype != torch.int32 or tuple(cu_seqlens_q.shape) != (batch + 1,)
+                or not cu_seqlens_q.is_contiguous() or cu_seqlens_q.device != dev):
+            raise ValueError(f"cu_seqlens_q must be a contiguous int32 [{batch + 1}] tensor on {dev}")
+        if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+            raise ValueError("slot_mapping must be a contiguous int64 vector")
+        T = slot_mapping.numel()
+        self.lib = lib = _lib.load()
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+        self.calls = []
+        for layer, cache in enumerate(caches):
+            qq, kk, vv, oo = q[layer], key[layer], value[layer], out[layer]
+            hq = qq.shape[1]
+            for name, t, shape in (("q", qq, (T, hq, cache.head_dim)), ("out", oo, (T, hq, cache.head_dim)),
+                                   ("key", kk, (T, cache.num_kv_heads, cache.head_dim)),
+                                   ("value", vv, (T, cache.num_kv_heads, cache.head_dim))):
+                if t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous() or t.device != dev:
+                    raise ValueError(f"layer {layer}: {name} must be a contiguous bfloat16 {shape} tensor on {dev}")
+            desc = ctypes.byref(cache.descriptor())
+            kv = (kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0), vv.stride(1),
+                  slot_mapping.data_ptr())
+            tail = (qq.data_ptr(), qq.stride(0), qq.stride(1), oo.data_ptr(), oo.stride(0), oo.stride(1), hq,
+                    cu_seqlens_q.data_ptr(), self.seq_lens.data_ptr(), self.block_table.data_ptr(),
+                    self.block_table.stride(0), self.block_table.shape[1], batch, int(max_query_len),
+                    int(max_seq_len), ctypes.c_float(scale), self.stream)
+            fn = lib.wkv_append_fp8 if cache.kv_dtype == "fp8_e4m3" else lib.wkv_append
+            self.calls.append((fn, (desc, *kv, T, self.stream), (desc, *kv, T, *tail),
+                               (desc, None, 0, 0, None, 0, 0, None, 0, *tail)))
+        self._keep = (caches, q, key, value, out, cu_seqlens_q, slot_mapping)
+
+    def append(self, layer: int) -> None:
+        fn, args, _, _ = self.calls[layer]
+        rc = fn(*args)
+        if rc:
+            _lib.check(rc, f"append layer {layer}")
+
+    def attend(self, layer: int) -> None:
+        rc = self.lib.wkv_prefill_gqa(*self.calls[layer][3])
+        if rc:
+            _lib.check(rc, f"prefill layer {layer}")
+
+    def step_layer(self, layer: int) -> None:
+        """Append + causal attention of one layer (two launches: the append, then the attention)."""
+        rc = self.lib.wkv_prefill_gqa(*self.calls[layer][2])
+        if rc:
+            _lib.check(rc, f"append+prefill layer {layer}")
+
+    def run(self) -> None:
+        for layer in range(len(self.calls)):
+            self.step_layer(layer)
