@@ -10,15 +10,19 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
 * ``prefill_gqa`` -- varlen (chunked) prefill that appends the prompt's K/V
   and attends causally over the paged context;
 * ``BlockManager`` -- host-side block allocation with ref-counted prefix
-  sharing for GRPO groups.
+  sharing for GRPO groups;
+* ``KVPool`` -- all layers' caches plus the block manager, with the engine's
+  sleep / wake_up lifecycle and KV metrics.
 """
 
 from .attention import paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla, prefill_gqa
 from .blocks import BlockManager
 from .cache import MLALatentCache, PagedKVCache, validate_tables
+from .pool import KVPool
 
 __all__ = [
     "BlockManager",
+    "KVPool",
     "MLALatentCache",
     "PagedKVCache",
     "paged_decode_gqa",

@@ -199,6 +199,13 @@ class BlockManager:
         for b in reversed(seq.blocks):
             self._release(b)
 
+    def sleep(self) -> None:
+        """Before the pool's memory is released (the engine's sleep, engine.py:858-869):
+        forget every cached prompt block; refuses while sequences still hold blocks."""
+        if self._seqs:
+            raise RuntimeError(f"{len(self._seqs)} sequences still hold KV blocks: finish or free them before sleep")
+        self.reset_prefix_cache()
+
     def reset_prefix_cache(self) -> None:
         """Forget every cached prompt block (engine.py:864, :1236-1242); live tables are untouched."""
         for b in self._evictable:

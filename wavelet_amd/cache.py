@@ -83,13 +83,17 @@ class PagedKVCache:
         self.num_kv_heads = int(num_kv_heads)
         self.head_dim = int(head_dim)
         self.kv_dtype = kv_dtype
-        fp8 = kv_dtype == "fp8_e4m3"
+        self._allocate()
+
+    def _allocate(self) -> None:
+        fp8 = self.kv_dtype == "fp8_e4m3"
         elem = torch.uint8 if fp8 else torch.bfloat16
         x = 16 if fp8 else 8
-        self.k = torch.zeros((num_blocks, num_kv_heads, head_dim // x, block_size, x), dtype=elem, device=self.device)
-        self.v = torch.zeros((num_blocks, num_kv_heads, head_dim, block_size), dtype=elem, device=self.device)
-        self.k_scale = torch.zeros((num_blocks, num_kv_heads), dtype=torch.float32, device=self.device) if fp8 else None
-        self.v_scale = torch.zeros((num_blocks, num_kv_heads), dtype=torch.float32, device=self.device) if fp8 else None
+        nb, h, d, bs = self.num_blocks, self.num_kv_heads, self.head_dim, self.block_size
+        self.k = torch.zeros((nb, h, d // x, bs, x), dtype=elem, device=self.device)
+        self.v = torch.zeros((nb, h, d, bs), dtype=elem, device=self.device)
+        self.k_scale = torch.zeros((nb, h), dtype=torch.float32, device=self.device) if fp8 else None
+        self.v_scale = torch.zeros((nb, h), dtype=torch.float32, device=self.device) if fp8 else None
         self._desc = _lib.WkvCache(
             k=self.k.data_ptr(),
             v=self.v.data_ptr(),
@@ -99,8 +103,24 @@ class PagedKVCache:
             block_size=self.block_size,
             num_kv_heads=self.num_kv_heads,
             head_dim=self.head_dim,
-            kv_dtype=KV_DTYPES[kv_dtype],
+            kv_dtype=KV_DTYPES[self.kv_dtype],
         )
+
+    # -- sleep / wake (the engine's sleep(level=1) / wake_up(tags=["kv_cache"]),
+    #    wavelet/inference/engine.py:858-873) ---------------------------------
+    @property
+    def asleep(self) -> bool:
+        return self._desc is None
+
+    def sleep(self) -> None:
+        """Release the pool's device memory; the contents are discarded."""
+        self.k = self.v = self.k_scale = self.v_scale = None
+        self._desc = None
+
+    def wake_up(self) -> None:
+        """Allocate the pool again (zeroed); a no-op when awake."""
+        if self.asleep:
+            self._allocate()
 
     # -- properties ---------------------------------------------------------
     @property
@@ -110,12 +130,16 @@ class PagedKVCache:
 
     @property
     def nbytes(self) -> int:
-        n = self.k.numel() * self.k.element_size() + self.v.numel() * self.v.element_size()
-        if self.k_scale is not None:
-            n += 2 * self.k_scale.numel() * 4
+        """Device bytes the pool holds while awake."""
+        elem = 1 if self.kv_dtype == "fp8_e4m3" else 2
+        n = 2 * self.num_blocks * self.num_kv_heads * self.head_dim * self.block_size * elem
+        if self.kv_dtype == "fp8_e4m3":
+            n += 2 * self.num_blocks * self.num_kv_heads * 4
         return n
 
     def descriptor(self) -> ctypes.Structure:
+        if self._desc is None:
+            raise RuntimeError("the KV cache is asleep: call wake_up() first")
         return self._desc
 
     # -- operations ---------------------------------------------------------
@@ -135,7 +159,7 @@ class PagedKVCache:
         lib = _lib.load()
         fn = lib.wkv_append_fp8 if self.kv_dtype == "fp8_e4m3" else lib.wkv_append
         rc = fn(
-            ctypes.byref(self._desc),
+            ctypes.byref(self.descriptor()),
             key.data_ptr(), key.stride(0), key.stride(1),
             value.data_ptr(), value.stride(0), value.stride(1),
             slots.data_ptr(), n, _stream(self.device),
@@ -171,7 +195,7 @@ class PagedKVCache:
         if total == 0 or batch == 0:
             return out_k, out_v
         rc = _lib.load().wkv_gather(
-            ctypes.byref(self._desc),
+            ctypes.byref(self.descriptor()),
             block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
             seq_lens.data_ptr(), cu.data_ptr(), batch,
             out_k.data_ptr(), out_v.data_ptr(), int(dequant), _stream(self.device),
@@ -185,7 +209,7 @@ class PagedKVCache:
         if block_mapping.dtype != torch.int64 or block_mapping.dim() != 2 or block_mapping.shape[1] != 2:
             raise ValueError("block_mapping must be int64 [n, 2]")
         m = block_mapping.contiguous()
-        rc = _lib.load().wkv_copy_blocks(ctypes.byref(self._desc), m.data_ptr(), m.shape[0], _stream(self.device))
+        rc = _lib.load().wkv_copy_blocks(ctypes.byref(self.descriptor()), m.data_ptr(), m.shape[0], _stream(self.device))
         _lib.check(rc, "copy_blocks")
 
 
@@ -203,8 +227,11 @@ class MLALatentCache:
         self.block_size = int(block_size)
         self.kv_lora_rank = int(kv_lora_rank)
         self.rope_dim = int(rope_dim)
-        self.latent = torch.zeros((num_blocks, block_size, kv_lora_rank + rope_dim), dtype=torch.bfloat16,
-                                  device=self.device)
+        self._allocate()
+
+    def _allocate(self) -> None:
+        self.latent = torch.zeros((self.num_blocks, self.block_size, self.kv_lora_rank + self.rope_dim),
+                                  dtype=torch.bfloat16, device=self.device)
         self._desc = _lib.WkvMlaCache(
             latent=self.latent.data_ptr(),
             num_blocks=self.num_blocks,
@@ -214,10 +241,30 @@ class MLALatentCache:
         )
 
     @property
+    def asleep(self) -> bool:
+        return self._desc is None
+
+    def sleep(self) -> None:
+        """Release the latent pool's device memory; the contents are discarded."""
+        self.latent = None
+        self._desc = None
+
+    def wake_up(self) -> None:
+        """Allocate the latent pool again (zeroed); a no-op when awake."""
+        if self.asleep:
+            self._allocate()
+
+    @property
     def capacity_tokens(self) -> int:
         return self.num_blocks * self.block_size
 
+    @property
+    def nbytes(self) -> int:
+        return self.num_blocks * self.block_size * (self.kv_lora_rank + self.rope_dim) * 2
+
     def descriptor(self) -> ctypes.Structure:
+        if self._desc is None:
+            raise RuntimeError("the KV cache is asleep: call wake_up() first")
         return self._desc
 
     def append(self, kv_c: torch.Tensor, k_pe: torch.Tensor, slot_mapping: torch.Tensor) -> None:
@@ -235,7 +282,7 @@ class MLALatentCache:
         n = kv_c.shape[0]
         slots = _slots(slot_mapping, n, self.device)
         rc = _lib.load().wkv_mla_append(
-            ctypes.byref(self._desc), kv_c.data_ptr(), kv_c.stride(0), k_pe.data_ptr(), k_pe.stride(0),
+            ctypes.byref(self.descriptor()), kv_c.data_ptr(), kv_c.stride(0), k_pe.data_ptr(), k_pe.stride(0),
             slots.data_ptr(), n, _stream(self.device),
         )
         _lib.check(rc, "mla_append")
