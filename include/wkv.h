@@ -221,6 +221,33 @@ int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_t key_strid
                     int32_t max_blocks_per_seq, int32_t batch, int32_t max_query_len, int32_t max_seq_len,
                     float scale, void *stream);
 
+/* Token sampler: the step after decode, producing what the engine records per
+ * generated token -- the token, its processed logprob and the sampling mask
+ * (llm.generate with logprobs_mode="processed_logprobs" and
+ * return_sampling_mask, engine.py:795-805, consumed at engine.py:187-256).
+ * logits [batch, vocab] (row_stride elements apart; logits_dtype 0 = fp32,
+ * 1 = bf16). Per row, in order (NULL arrays = the default):
+ *   repetition penalty on tokens set in seen_tokens (bitmap, [batch,
+ *   ceil(vocab/32)] uint32): l > 0 ? l / r : l * r (default r = 1);
+ *   x = l / temperature (temperature < 1e-5: greedy, x = l; default 1);
+ *   min_p: keep x >= max(x) + ln(min_p) (default 0: off);
+ *   top_k: keep the top_k largest, ties kept (<= 0 or >= vocab: off);
+ *   top_p: keep token i iff the softmax mass of tokens strictly larger than
+ *     x_i is < top_p (>= 1: off);
+ *   sample: exponential race over the kept set, E_i ~ Exp(1) from a hash of
+ *     (seeds[b], step, i) -- a draw from softmax(x) restricted to the kept set;
+ *     greedy rows take the largest x (ties: lowest index).
+ * Outputs: out_tokens [batch] int64; out_logprobs [batch] (log-softmax of x
+ * over the kept set at the token; may be NULL); out_mask [batch,
+ * ceil(vocab/32)] bitmap of the kept set and out_counts [batch] its size
+ * (each may be NULL). Deterministic for given inputs and step.
+ * Replaces vLLM's sampler (vllm.v1 Sampler; parameters from
+ * vllm_sampling_kwargs, engine.py:69-90). */
+int wkv_sample(const void *logits, int32_t logits_dtype, int64_t row_stride, int32_t batch, int32_t vocab,
+               const float *temperature, const int32_t *top_k, const float *top_p, const float *min_p,
+               const float *repetition_penalty, const uint32_t *seen_tokens, const uint64_t *seeds, int64_t step,
+               int64_t *out_tokens, float *out_logprobs, uint32_t *out_mask, int32_t *out_counts, void *stream);
+
 /* Weight-absorbed MLA decode over the latent cache:
  *   s = (q_nope . c_kv + q_pe . k_pe) * scale; o = softmax(s) . c_kv
  * q_nope [batch, num_heads, kv_lora_rank], q_pe [batch, num_heads, rope_dim]

@@ -12,13 +12,16 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
 * ``BlockManager`` -- host-side block allocation with ref-counted prefix
   sharing for GRPO groups;
 * ``KVPool`` -- all layers' caches plus the block manager, with the engine's
-  sleep / wake_up lifecycle and KV metrics.
+  sleep / wake_up lifecycle and KV metrics;
+* ``sample`` -- the token sampler after decode (temperature, min_p, top_k,
+  top_p, repetition penalty; processed logprobs and the sampling mask).
 """
 
 from .attention import paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla, prefill_gqa
 from .blocks import BlockManager
 from .cache import MLALatentCache, PagedKVCache, validate_tables
 from .pool import KVPool
+from .sampler import sample
 
 __all__ = [
     "BlockManager",
@@ -29,5 +32,6 @@ __all__ = [
     "paged_decode_gqa_grouped",
     "paged_decode_mla",
     "prefill_gqa",
+    "sample",
     "validate_tables",
 ]

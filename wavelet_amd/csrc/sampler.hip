@@ -1,0 +1,327 @@
+// Token sampler for gfx950: the step after the last layer's decode.
+//
+// One workgroup (1024 threads) per row of logits, passes over the row (L2 /
+// MALL resident after the first):
+//   x_i = (repetition penalty on seen tokens)(logit_i) / T   (T = 1 for greedy rows)
+//   min_p:  keep x_i >= max + ln(min_p)             (p_i >= min_p * p_max)
+//   top_k:  keep the k largest (exact radix select over order-preserving
+//           32-bit keys, four 8-bit rounds, LDS histograms; ties kept)
+//   top_p:  keep token i iff the mass strictly above it is < top_p * mass
+//           (radix select over the same keys with 64-bit fixed-point mass
+//           histograms -- integer sums, so the threshold is deterministic)
+//   sample: argmax over kept i of x_i - ln(E_i), E_i ~ Exp(1) from a
+//           counter-based hash of (seed, step, i) -- the exponential race,
+//           an exact draw from softmax over the kept set; greedy rows take
+//           argmax x_i. Ties go to the lowest index.
+// Outputs: the token, its processed logprob (log-softmax over the kept set of
+// the processed logits), the kept set as a bitmap and its size.
+#include <cmath>
+
+#include "wkv_common.h"
+
+namespace wkv {
+
+constexpr int kSampleThreads = 1024;
+constexpr float kGreedyEps = 1e-5f;  // temperatures below this sample greedily
+
+// Order-preserving key of a float (larger float -> larger key); NaN maps below
+// every real value so it is never kept.
+__device__ __forceinline__ uint32_t order_key(float x) {
+  if (x != x) return 0u;
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// splitmix64 finaliser.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// ln(E) of the Exp(1) variate of token i: u in (0, 1) from 24 hash bits.
+__device__ __forceinline__ float log_exp_variate(uint64_t stream, int64_t i) {
+  const uint64_t h = mix64(stream + static_cast<uint64_t>(i));
+  const float u = (static_cast<float>(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+  return logf(-logf(u));
+}
+
+template <typename T>
+__device__ __forceinline__ float load_logit(const T *row, int64_t i);
+template <>
+__device__ __forceinline__ float load_logit<float>(const float *row, int64_t i) { return row[i]; }
+template <>
+__device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *row, int64_t i) {
+  return bf16_bits_to_f32(row[i]);
+}
+
+// Block-wide reductions over 1024 threads (16 waves) through a small LDS array.
+__device__ __forceinline__ float block_max(float v, float *red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < kSampleThreads / 64; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int i = 0; i < kSampleThreads / 64; ++i) r += red[i];  // fixed order: deterministic
+  __syncthreads();
+  return r;
+}
+
+// (value, index) argmax, ties to the lowest index.
+__device__ __forceinline__ void arg_better(float &v, int64_t &i, float ov, int64_t oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+__device__ __forceinline__ void block_argmax(float &v, int64_t &idx, float *redv, int64_t *redi) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int64_t oi = __shfl_xor(idx, o, 64);
+    arg_better(v, idx, ov, oi);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    redv[w] = v;
+    redi[w] = idx;
+  }
+  __syncthreads();
+  v = redv[0];
+  idx = redi[0];
+  for (int i = 1; i < kSampleThreads / 64; ++i) arg_better(v, idx, redv[i], redi[i]);
+  __syncthreads();
+}
+
+struct SampleArgs {
+  const float *temperature;  // [B] or NULL (1.0)
+  const int32_t *top_k;      // [B] or NULL; <= 0 or >= vocab: off
+  const float *top_p;        // [B] or NULL; >= 1: off
+  const float *min_p;        // [B] or NULL; <= 0: off
+  const float *rep_penalty;  // [B] or NULL; 1: off
+  const uint32_t *seen;      // [B, words] bitmap of prompt/output tokens or NULL
+  const uint64_t *seeds;     // [B] or NULL (0)
+  int64_t step;              // mixed into every row's random stream
+  int64_t *tokens;           // [B]
+  float *logprobs;           // [B] or NULL
+  uint32_t *mask;            // [B, words] or NULL
+  int32_t *counts;           // [B] or NULL
+};
+
+template <typename T>
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restrict__ logits, int64_t row_stride,
+                                                                int vocab, SampleArgs a) {
+  __shared__ float redv[kSampleThreads / 64];
+  __shared__ int64_t redi[kSampleThreads / 64];
+  __shared__ unsigned long long hist[256];
+  __shared__ uint32_t sel_prefix;
+  __shared__ unsigned long long sel_above;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const T *row = logits + static_cast<int64_t>(b) * row_stride;
+  const int words = (vocab + 31) / 32;
+  const float temp = a.temperature ? a.temperature[b] : 1.f;
+  const bool greedy = temp < kGreedyEps;
+  const float inv_t = greedy ? 1.f : 1.f / temp;
+  const float pen = a.rep_penalty ? a.rep_penalty[b] : 1.f;
+  const uint32_t *seen = (a.seen && pen != 1.f) ? a.seen + static_cast<int64_t>(b) * words : nullptr;
+  auto x_of = [&](int64_t i) {
+    float l = load_logit<T>(row, i);
+    if (seen && ((seen[i >> 5] >> (i & 31)) & 1u)) l = l > 0.f ? l / pen : l * pen;
+    return l * inv_t;
+  };
+
+  // Pass 1: max (and the greedy argmax).
+  float mx = -INFINITY;
+  int64_t amx = 0x7fffffffffffffffll;
+  for (int64_t i = tid; i < vocab; i += kSampleThreads) arg_better(mx, amx, x_of(i), i);
+  block_argmax(mx, amx, redv, redi);
+  if (!(mx > -INFINITY)) {  // nothing finite: token 0, empty support
+    if (tid == 0) {
+      a.tokens[b] = 0;
+      if (a.logprobs) a.logprobs[b] = -INFINITY;
+      if (a.counts) a.counts[b] = 0;
+    }
+    if (a.mask)
+      for (int wd = tid; wd < words; wd += kSampleThreads) a.mask[static_cast<int64_t>(b) * words + wd] = 0u;
+    return;
+  }
+  // min_p as a key threshold: x >= max + ln(min_p).
+  const float mp = a.min_p ? a.min_p[b] : 0.f;
+  uint32_t key_lo = order_key(-3.402823466e38f);  // finite values only
+  if (mp > 0.f) {
+    const uint32_t k = order_key(mx + logf(mp));
+    key_lo = k > key_lo ? k : key_lo;
+  }
+
+  // top_k: radix select of the k-th largest key among kept tokens.
+  const int topk = a.top_k ? a.top_k[b] : 0;
+  if (topk > 0 && topk < vocab) {
+    uint32_t prefix = 0, pmask = 0;
+    unsigned long long remaining = static_cast<unsigned long long>(topk);
+    bool enough = true;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
+      __syncthreads();
+      for (int64_t i = tid; i < vocab; i += kSampleThreads) {
+        const uint32_t k = order_key(x_of(i));
+        if (k >= key_lo && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1ull);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        unsigned long long cum = 0;
+        int bin = -1;
+        for (int j = 255; j >= 0; --j) {
+          if (cum + hist[j] >= remaining) {
+            bin = j;
+            break;
+          }
+          cum += hist[j];
+        }
+        sel_prefix = static_cast<uint32_t>(bin);  // -1: fewer than k kept tokens
+        sel_above = cum;
+      }
+      __syncthreads();
+      const int bin = static_cast<int>(sel_prefix);
+      const unsigned long long above = sel_above;
+      __syncthreads();
+      if (bin < 0) {
+        enough = false;
+        break;
+      }
+      remaining -= above;
+      prefix |= static_cast<uint32_t>(bin) << shift;
+      pmask |= 255u << shift;
+    }
+    if (enough && prefix > key_lo) key_lo = prefix;
+  }
+
+  // top_p: radix select over fixed-point mass w_i = exp(x_i - max) * 2^32.
+  const float tp = a.top_p ? a.top_p[b] : 1.f;
+  if (tp < 1.f) {
+    unsigned long long total = 0;
+    {
+      // total kept mass (integer: exact, order-independent)
+      for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
+      __syncthreads();
+      unsigned long long part = 0;
+      for (int64_t i = tid; i < vocab; i += kSampleThreads) {
+        const float x = x_of(i);
+        if (order_key(x) >= key_lo) part += static_cast<unsigned long long>(expf(x - mx) * 4294967296.f);
+      }
+      atomicAdd(&hist[0], part);
+      __syncthreads();
+      total = hist[0];
+      __syncthreads();
+    }
+    const unsigned long long target =
+        static_cast<unsigned long long>(ceil(static_cast<double>(tp) * static_cast<double>(total)));
+    uint32_t prefix = 0, pmask = 0;
+    unsigned long long above = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
+      __syncthreads();
+      for (int64_t i = tid; i < vocab; i += kSampleThreads) {
+        const float x = x_of(i);
+        const uint32_t k = order_key(x);
+        if (k >= key_lo && (k & pmask) == prefix)
+          atomicAdd(&hist[(k >> shift) & 255u], static_cast<unsigned long long>(expf(x - mx) * 4294967296.f));
+      }
+      __syncthreads();
+      if (tid == 0) {
+        unsigned long long cum = above;
+        int bin = 0;
+        for (int j = 255; j >= 0; --j) {
+          if (cum + hist[j] >= target) {
+            bin = j;
+            break;
+          }
+          cum += hist[j];
+        }
+        sel_prefix = static_cast<uint32_t>(bin);
+        sel_above = cum;
+      }
+      __syncthreads();
+      prefix |= sel_prefix << shift;
+      above = sel_above;
+      pmask |= 255u << shift;
+      __syncthreads();
+    }
+    if (prefix > key_lo) key_lo = prefix;
+  }
+
+  // Final pass: kept mass, the draw, the mask bitmap and the support size.
+  const uint64_t stream = mix64((a.seeds ? a.seeds[b] : 0ull) + static_cast<uint64_t>(a.step) * 0x9E3779B97F4A7C15ull);
+  float z = 0.f, best = -INFINITY;
+  int64_t bi = 0x7fffffffffffffffll;
+  int cnt = 0;
+  for (int64_t base = 0; base < vocab; base += kSampleThreads) {
+    const int64_t i = base + tid;
+    bool kept = false;
+    if (i < vocab) {
+      const float x = x_of(i);
+      kept = order_key(x) >= key_lo;
+      if (kept) {
+        z += expf(x - mx);
+        ++cnt;
+        const float score = greedy ? x : x - log_exp_variate(stream, i);
+        arg_better(best, bi, score, i);
+      }
+    }
+    if (a.mask) {
+      const unsigned long long bal = __ballot(kept);
+      const int lane = tid & 63;
+      if (lane == 0 || lane == 32) {
+        const int64_t wd = (base + (tid & ~31)) >> 5;
+        if (wd < words) a.mask[static_cast<int64_t>(b) * words + wd] = static_cast<uint32_t>(bal >> lane);
+      }
+    }
+  }
+  z = block_sum(z, redv);
+  block_argmax(best, bi, redv, redi);
+  const float c = block_sum(static_cast<float>(cnt), redv);
+  if (tid == 0) {
+    a.tokens[b] = bi;
+    if (a.logprobs) a.logprobs[b] = (x_of(bi) - mx) - logf(z);
+    if (a.counts) a.counts[b] = static_cast<int32_t>(c);
+  }
+}
+
+}  // namespace wkv
+
+using namespace wkv;
+
+extern "C" int wkv_sample(const void *logits, int32_t logits_dtype, int64_t row_stride, int32_t batch, int32_t vocab,
+                          const float *temperature, const int32_t *top_k, const float *top_p, const float *min_p,
+                          const float *repetition_penalty, const uint32_t *seen_tokens, const uint64_t *seeds,
+                          int64_t step, int64_t *out_tokens, float *out_logprobs, uint32_t *out_mask,
+                          int32_t *out_counts, void *stream) {
+  WKV_CHECK_ARG(batch >= 0, "batch must be >= 0");
+  if (batch == 0) return WKV_OK;
+  WKV_CHECK_ARG(vocab > 0 && vocab < (1 << 24), "vocab must be in [1, 2^24) (got %d)", vocab);
+  WKV_CHECK_ARG(logits != nullptr && out_tokens != nullptr, "logits / out_tokens is NULL");
+  WKV_CHECK_ARG(logits_dtype == 0 || logits_dtype == 1, "logits_dtype must be 0 (fp32) or 1 (bf16)");
+  WKV_CHECK_ARG(row_stride >= vocab, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+  SampleArgs a{temperature, top_k, top_p, min_p, repetition_penalty, seen_tokens, seeds, step,
+               out_tokens, out_logprobs, out_mask, out_counts};
+  auto s = static_cast<hipStream_t>(stream);
+  if (logits_dtype == 0)
+    sample_kernel<float><<<batch, kSampleThreads, 0, s>>>(static_cast<const float *>(logits), row_stride, vocab, a);
+  else
+    sample_kernel<uint16_t><<<batch, kSampleThreads, 0, s>>>(static_cast<const uint16_t *>(logits), row_stride,
+                                                              vocab, a);
+  WKV_CHECK_LAUNCH("sample");
+  return WKV_OK;
+}
