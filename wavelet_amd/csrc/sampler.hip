@@ -55,6 +55,34 @@ __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *row, int64
   return bf16_bits_to_f32(row[i]);
 }
 
+// Elements per thread per step: 8 consecutive logits, one or two 16-byte loads
+// when the row allows it (`vec`), element loads otherwise; -inf past the end.
+constexpr int kVec = 8;
+template <typename T>
+__device__ __forceinline__ void load8(float v[kVec], const T *row, int64_t base, int vocab, bool vec) {
+  if (vec && base + kVec <= vocab) {
+    if constexpr (sizeof(T) == 2) {
+      const u32x4 w = *reinterpret_cast<const u32x4 *>(row + base);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(w[j] << 16);
+        v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      }
+    } else {
+      const floatx4 a = *reinterpret_cast<const floatx4 *>(row + base);
+      const floatx4 b = *reinterpret_cast<const floatx4 *>(row + base + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = a[j];
+        v[4 + j] = b[j];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) v[j] = base + j < vocab ? load_logit<T>(row, base + j) : -INFINITY;
+  }
+}
+
 // Block-wide reductions over 1024 threads (16 waves) through a small LDS array.
 __device__ __forceinline__ float block_max(float v, float *red) {
   v = wave_max(v);
@@ -137,16 +165,35 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   const float inv_t = greedy ? 1.f : 1.f / temp;
   const float pen = a.rep_penalty ? a.rep_penalty[b] : 1.f;
   const uint32_t *seen = (a.seen && pen != 1.f) ? a.seen + static_cast<int64_t>(b) * words : nullptr;
+  const bool vec = (row_stride % kVec) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0;
   auto x_of = [&](int64_t i) {
     float l = load_logit<T>(row, i);
     if (seen && ((seen[i >> 5] >> (i & 31)) & 1u)) l = l > 0.f ? l / pen : l * pen;
     return l * inv_t;
   };
+  // The 8 processed logits at base .. base+7 (-inf past the end).
+  auto x8 = [&](float v[kVec], int64_t base) {
+    load8<T>(v, row, base, vocab, vec);
+    if (seen) {
+      const uint32_t w = seen[base >> 5] >> (base & 31);  // base is a multiple of 8: one word
+#pragma unroll
+      for (int j = 0; j < kVec; ++j)
+        if ((w >> j) & 1u) v[j] = v[j] > 0.f ? v[j] / pen : v[j] * pen;
+    }
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) v[j] *= inv_t;
+  };
+  const int64_t step8 = static_cast<int64_t>(kSampleThreads) * kVec;
 
   // Pass 1: max (and the greedy argmax).
   float mx = -INFINITY;
   int64_t amx = 0x7fffffffffffffffll;
-  for (int64_t i = tid; i < vocab; i += kSampleThreads) arg_better(mx, amx, x_of(i), i);
+  for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
+    float v[kVec];
+    x8(v, base);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) arg_better(mx, amx, v[j], base + j);
+  }
   block_argmax(mx, amx, redv, redi);
   if (!(mx > -INFINITY)) {  // nothing finite: token 0, empty support
     if (tid == 0) {
@@ -175,9 +222,14 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
       __syncthreads();
-      for (int64_t i = tid; i < vocab; i += kSampleThreads) {
-        const uint32_t k = order_key(x_of(i));
-        if (k >= key_lo && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1ull);
+      for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
+        float v[kVec];
+        x8(v, base);
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+          const uint32_t k = order_key(v[j]);
+          if (k >= key_lo && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1ull);
+        }
       }
       __syncthreads();
       if (tid == 0) {
@@ -217,9 +269,12 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
       for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
       __syncthreads();
       unsigned long long part = 0;
-      for (int64_t i = tid; i < vocab; i += kSampleThreads) {
-        const float x = x_of(i);
-        if (order_key(x) >= key_lo) part += static_cast<unsigned long long>(expf(x - mx) * 4294967296.f);
+      for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
+        float v[kVec];
+        x8(v, base);
+#pragma unroll
+        for (int j = 0; j < kVec; ++j)
+          if (order_key(v[j]) >= key_lo) part += static_cast<unsigned long long>(expf(v[j] - mx) * 4294967296.f);
       }
       atomicAdd(&hist[0], part);
       __syncthreads();
@@ -233,11 +288,15 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
       __syncthreads();
-      for (int64_t i = tid; i < vocab; i += kSampleThreads) {
-        const float x = x_of(i);
-        const uint32_t k = order_key(x);
-        if (k >= key_lo && (k & pmask) == prefix)
-          atomicAdd(&hist[(k >> shift) & 255u], static_cast<unsigned long long>(expf(x - mx) * 4294967296.f));
+      for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
+        float v[kVec];
+        x8(v, base);
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+          const uint32_t k = order_key(v[j]);
+          if (k >= key_lo && (k & pmask) == prefix)
+            atomicAdd(&hist[(k >> shift) & 255u], static_cast<unsigned long long>(expf(v[j] - mx) * 4294967296.f));
+        }
       }
       __syncthreads();
       if (tid == 0) {
@@ -267,26 +326,29 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   float z = 0.f, best = -INFINITY;
   int64_t bi = 0x7fffffffffffffffll;
   int cnt = 0;
-  for (int64_t base = 0; base < vocab; base += kSampleThreads) {
-    const int64_t i = base + tid;
-    bool kept = false;
-    if (i < vocab) {
-      const float x = x_of(i);
-      kept = order_key(x) >= key_lo;
-      if (kept) {
-        z += expf(x - mx);
-        ++cnt;
-        const float score = greedy ? x : x - log_exp_variate(stream, i);
-        arg_better(best, bi, score, i);
+  for (int64_t c0 = 0; c0 < vocab; c0 += step8) {  // uniform trip count: every lane shuffles below
+    const int64_t base = c0 + static_cast<int64_t>(tid) * kVec;
+    uint32_t bits = 0;
+    if (base < vocab) {
+      float v[kVec];
+      x8(v, base);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        if (order_key(v[j]) >= key_lo) {
+          bits |= 1u << j;
+          z += expf(v[j] - mx);
+          ++cnt;
+          const float score = greedy ? v[j] : v[j] - log_exp_variate(stream, base + j);
+          arg_better(best, bi, score, base + j);
+        }
       }
     }
     if (a.mask) {
-      const unsigned long long bal = __ballot(kept);
-      const int lane = tid & 63;
-      if (lane == 0 || lane == 32) {
-        const int64_t wd = (base + (tid & ~31)) >> 5;
-        if (wd < words) a.mask[static_cast<int64_t>(b) * words + wd] = static_cast<uint32_t>(bal >> lane);
-      }
+      // four consecutive lanes hold the 32 bits of one mask word
+      const uint32_t b1 = __shfl_down(bits, 1, 64), b2 = __shfl_down(bits, 2, 64), b3 = __shfl_down(bits, 3, 64);
+      const int64_t wd = base >> 5;
+      if ((tid & 3) == 0 && wd < words)
+        a.mask[static_cast<int64_t>(b) * words + wd] = bits | (b1 << 8) | (b2 << 16) | (b3 << 24);
     }
   }
   z = block_sum(z, redv);
