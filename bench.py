@@ -38,7 +38,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="qwen3-4b",
                     choices=["qwen3-4b", "qwen3-4b-var", "qwen2.5-0.5b", "qwen2.5-7b-groups", "deepseek-v3-mla",
-                             "qwen3-4b-prefill"],
+                             "qwen3-4b-prefill", "sampler"],
                     help="qwen3-4b is the headline; the others are the remaining measured shapes")
     ap.add_argument("--layers", type=int, default=0, help="0 = the model's depth (8 rotated layers for MLA)")
     ap.add_argument("--batch", type=int, default=64)
@@ -291,6 +291,43 @@ def workload(args, torch, dev) -> dict:
                 "flops_per_layer": flops, "cache_bytes": caches[0].nbytes, "bound": "mfma",
                 "desc": f"Qwen3-4B prompt step: {args.layers} layers x (append + causal prefill attention), "
                         f"{B} prompts x {n_new} tokens, 32 q / 8 kv heads, d=128, bf16, block 16"}
+    elif name == "sampler":
+        # the step after decode: one token per row from bf16 logits over Qwen's vocabulary,
+        # temperature 0.7, top_k 50, top_p 0.9, with processed logprobs and the sampling mask
+        from wavelet_amd import sample
+
+        B, V = 256, 151936
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1234)
+        logits = (torch.randn((B, V), generator=gen, device=dev) * 4).to(torch.bfloat16)
+        seeds = torch.arange(B, dtype=torch.int64, device=dev)
+
+        class _Step:
+            grouped = False
+
+            def __init__(self):
+                self.n = 0
+
+            def step_layer(self, layer):
+                self.n += 1
+                sample(logits, temperature=0.7, top_k=50, top_p=0.9, seeds=seeds, step=self.n, return_mask=True)
+
+            attend = append = step_layer
+
+            def run(self):
+                self.step_layer(0)
+
+        args.layers = 1
+        w = synth.make_decode_workload(name, batch=B, num_kv_heads=1, num_q_heads=1, head_dim=64, block_size=16,
+                                       context_lens=np.ones(B))
+        words = (V + 31) // 32
+        nbytes = B * V * 2 + B * (8 + 4 + 4) + B * words * 4
+        return {"name": name, "step": _Step(), "w": w, "layer_bytes": nbytes, "attn_bytes": nbytes,
+                "kernel": "sample_kernel<bf16>", "dtype": "bf16 logits, fp32 math", "flops_per_layer": 0,
+                "metric": "sampler GB/s of logits & us/step, 256 x 151936",
+                "cache_bytes": B * V * 2,
+                "desc": f"token sampler: {B} rows x {V} bf16 logits, T=0.7, top_k=50, top_p=0.9, processed "
+                        "logprobs + sampling mask"}
     else:
         raise SystemExit(f"unknown workload {name}")
     L = w.context_lens.astype(np.int64)
@@ -392,7 +429,7 @@ def main() -> int:
         return 0
     rec = {
         "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx" if headline
-        else f"decode-attn+KV-append GB/s & us/step, {wl['name']}",
+        else wl.get("metric", f"decode-attn+KV-append GB/s & us/step, {wl['name']}"),
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
