@@ -551,13 +551,15 @@ struct GroupSlots {
   }
 };
 
-// Tokens per partition when the caller leaves it to the library: enough
-// work items to give every CU a full complement of resident waves in about
-// one round (fewer, longer waves amortise the per-wave prologue and the
-// partial-result traffic), at least 128 tokens, a multiple of the block size
-// (the fused append relies on it), and at most 64 blocks (one lane each).
-static int choose_partition(int batch, int hkv, int max_seq_len, int BS, int D) {
-  const int64_t target_waves = D == 128 ? 2048 : 4096;
+// Tokens per partition when the caller leaves it to the library: about 2,048
+// partition waves over the longest context -- every CU's resident slots in
+// about one round, and no more (fewer, longer waves amortise the per-wave
+// prologue and the partial-result traffic; measured, d=64 contexts of
+// 256..2,048 tokens run 8% faster at 2,048 than at 4,096 waves) -- at least
+// 128 tokens, a multiple of the block size (the fused append relies on it),
+// and at most 64 blocks (one lane each).
+static int choose_partition(int batch, int hkv, int max_seq_len, int BS) {
+  const int64_t target_waves = 2048;
   const int64_t items = static_cast<int64_t>(batch) * hkv;
   int64_t p = (items * max_seq_len + target_waves - 1) / target_waves;
   const int64_t unit = BS;  // a multiple of 16 already
@@ -612,7 +614,7 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   WKV_CHECK_ARG(max_seq_len >= 0, "max_seq_len must be >= 0");
   WKV_CHECK_ARG(std::isfinite(scale), "scale must be finite");
   const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
-  if (partition_size == 0) partition_size = choose_partition(batch, Hkv, max_seq, BS, D);
+  if (partition_size == 0) partition_size = choose_partition(batch, Hkv, max_seq, BS);
   WKV_CHECK_ARG(partition_size >= 16 && partition_size % 16 == 0, "partition_size must be a positive multiple of 16");
   WKV_CHECK_ARG((partition_size + BS - 17) / BS + 1 <= 64,
                 "partition_size %d spans more than 64 blocks of %d tokens", partition_size, BS);
@@ -683,8 +685,8 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
 // the suffix role's as many partitions.
 constexpr int kGroupW = 4;
 
-static int grouped_partition(int32_t partition_size, int batch, int hkv, int max_seq, int BS, int D) {
-  return partition_size != 0 ? partition_size : choose_partition(batch, hkv, max_seq, BS, D);
+static int grouped_partition(int32_t partition_size, int batch, int hkv, int max_seq, int BS) {
+  return partition_size != 0 ? partition_size : choose_partition(batch, hkv, max_seq, BS);
 }
 
 // Most tokens per prefix partition: about what the longest suffix gives each
@@ -741,7 +743,7 @@ static int launch_grouped(const wkv_cache_t *cache, const StepAppend *ap, const 
   WKV_CHECK_ARG(group_size >= 1 && group_size <= batch, "group_size must be in [1, batch] (got %d)", group_size);
   WKV_CHECK_ARG(max_prefix_len >= 0, "max_prefix_len must be >= 0");
   const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
-  const int P = grouped_partition(partition_size, batch, Hkv, max_seq, BS, D);
+  const int P = grouped_partition(partition_size, batch, Hkv, max_seq, BS);
   WKV_CHECK_ARG(P >= 16 && P % BS == 0, "partition_size %d must be a positive multiple of block_size %d", P, BS);
   WKV_CHECK_ARG(P / BS <= 64, "partition_size %d spans more than 64 blocks of %d tokens", P, BS);
   const int n_groups = (batch + group_size - 1) / group_size;

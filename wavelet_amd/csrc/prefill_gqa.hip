@@ -10,15 +10,54 @@
 // Work decomposition: workgroup (16-token query tile, KV head x head group,
 // sequence) of four waves; wave w takes query head kvh*G + 4*hg + w, so the
 // MFMA columns are 16 consecutive query tokens of one head and the four waves
-// of a workgroup stream the same key tiles (one HBM read, three cache hits).
-// Keys are streamed in 16-token tiles by the decode kernels' tile loop
-// (gqa_tiles.h), in ranges of 64 blocks; tiles on the causal diagonal mask per
-// lane (column). Every wave finishes its rows: no split-K, no workspace.
+// of a workgroup stream the same key tiles. Every query tile of a (sequence,
+// KV head) re-reads that head's keys, so the 1-D grid sends all of them to
+// one XCD (the dispatcher deals workgroup i to XCD i mod 8): the keys are
+// served from that XCD's L2 instead of being fetched by all eight. The
+// latest (most expensive, causally) query tiles are dispatched first.
+// Keys are streamed in 16-token tiles staged once per workgroup in LDS (double
+// buffered: every thread fetches its 16-byte pieces of tile i+1 while the
+// waves attend tile i from LDS with the decode kernels' tile arithmetic,
+// gqa_tiles.h); tiles on the causal diagonal mask per lane (column). Every
+// wave finishes its rows: no split-K, no workspace.
 #include "gqa_tiles.h"
 
 namespace wkv {
 
 constexpr int kPrefillWaves = 4;
+
+// One 16-token key tile of one (block, KV head) in LDS, in the cache's order:
+// K as [D/x chunks][16 tokens][16 bytes], V as [D rows][16 tokens x element].
+// A lane's MFMA operand is then one contiguous LDS read (K: 16 bytes of chunk
+// 4j+grp, token col; V: bf16 tokens 4grp..4grp+3 of row 16n+col, fp8 the
+// whole row 64j+16grp+col), and a wave's reads cover contiguous bytes.
+template <int D, bool FP8>
+struct LdsTile {
+  static constexpr int ESZ = FP8 ? 1 : 2;
+  static constexpr int KB = D * 16 * ESZ;  // K bytes
+  static constexpr int VB = D * 16 * ESZ;  // V bytes
+  static constexpr int BYTES = KB + VB;
+  static constexpr int PIECES = BYTES / 16;  // 16-byte pieces
+  static constexpr int PER_THREAD = (PIECES + 64 * kPrefillWaves - 1) / (64 * kPrefillWaves);
+  static constexpr bool EVEN = PIECES % (64 * kPrefillWaves) == 0;  // else the last round is partial
+};
+
+// Global address of 16-byte piece p of the tile (tokens o0..o0+15 of block
+// blk, KV head kvh) and its LDS offset (= 16 p).
+template <int D, bool FP8>
+__device__ __forceinline__ const uint8_t *tile_piece(const uint8_t *kc, const uint8_t *vc, int64_t rbase, int o0,
+                                                     int BS, int p) {
+  using T = LdsTile<D, FP8>;
+  if (p < T::KB / 16) {  // K chunk c, token m: 16 bytes at ((c*BS + o0 + m) * 16) of the region
+    const int c = p >> 4, m = p & 15;
+    return kc + rbase + (static_cast<int64_t>(c) * BS + o0 + m) * 16;
+  }
+  // V row d: the 16 tokens are 32 (bf16) or 16 (fp8) contiguous bytes
+  const int v = p - T::KB / 16;
+  constexpr int PPR = 16 * T::ESZ / 16;  // pieces per row
+  const int d = v / PPR, half = v % PPR;
+  return vc + rbase + (static_cast<int64_t>(d) * BS + o0) * T::ESZ + half * 16;
+}
 
 template <int D, bool FP8>
 __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
@@ -26,10 +65,18 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
     const float *__restrict__ vs, const uint16_t *__restrict__ q, int64_t q_st, int64_t q_sh,
     uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
     const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
-    int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2) {
-  const int qt = blockIdx.x, b = blockIdx.z;
-  const int kvh = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.y) / n_hg);
-  const int hg = static_cast<int>(blockIdx.y) - kvh * n_hg;
+    int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
+  using LT = LdsTile<D, FP8>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][LT::BYTES];
+  // Linear id = ((item / 8) * n_qt + (n_qt - 1 - qt)) * 8 + item % 8, item =
+  // (sequence, KV head, head group): the XCD (id % 8) depends on the item only.
+  const int id = blockIdx.x;
+  const int item = (id / (8 * n_qt)) * 8 + (id & 7);
+  const int qt = __builtin_amdgcn_readfirstlane(n_qt - 1 - (id / 8) % n_qt);
+  if (item >= n_items) return;
+  const int b = __builtin_amdgcn_readfirstlane(item / (Hkv * n_hg));
+  const int kvh = __builtin_amdgcn_readfirstlane((item / n_hg) % Hkv);
+  const int hg = item % n_hg;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int q0 = cu_q[b];
@@ -37,16 +84,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
   int L = seq_lens[b];
   L = L < max_seq ? L : max_seq;
   const int t0 = qt * 16;
+  if (t0 >= qlen) return;  // the whole workgroup leaves together
   const int h_local = hg * kPrefillWaves + wave;
-  if (t0 >= qlen || h_local >= G) return;  // no barrier in this kernel: waves leave independently
-  const int h = kvh * G + h_local;
+  const bool active = h_local < G;  // an idle wave still loads its share of every tile
+  const int h = kvh * G + (active ? h_local : 0);
   const int ctx = L - qlen;  // position of new token 0 (negative only for inconsistent inputs)
   const int tok = t0 + col;
-  const bool valid = tok < qlen;
+  const bool valid = active && tok < qlen;
   const int pos = ctx + tok;  // this column's position; it sees keys [0, pos]
 
   bf16x8 qop[D / 32];
-  load_q<D, FP8>(qop, q + static_cast<int64_t>(q0 + (valid ? tok : t0)) * q_st + static_cast<int64_t>(h) * q_sh,
+  load_q<D, FP8>(qop, q + static_cast<int64_t>(q0 + (tok < qlen ? tok : t0)) * q_st + static_cast<int64_t>(h) * q_sh,
                  valid, grp);
   DecodeState<D, FP8> st;
 #pragma unroll
@@ -54,26 +102,102 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
   st.m = -INFINITY;
   st.l = 0.f;
 
-  // Keys up to the tile's last query: [0, kend).
+  // Keys up to the tile's last query: [0, kend), in 16-token tiles.
   const int last = (t0 + 16 < qlen ? t0 + 16 : qlen) - 1;
   const int kend = ctx + last + 1;
-  const int span = 64 * BS;  // one attend_range: at most 64 blocks (one lane each)
-  for (int r0 = 0; r0 < kend; r0 += span) {
-    const int r1 = (r0 + span) < kend ? (r0 + span) : kend;
-    const int blk_first = r0 / BS;
-    int my_blk = -1;
-    if (blk_first + lane < Mb) my_blk = bt[b * bt_stride + blk_first + lane];
-    attend_range<D, FP8>(
-        [&](Tile<D, FP8> &t) {
-          int lim = pos - t.ts + 1;  // keys of the tile this column sees
-          lim = lim < 0 ? 0 : (lim > 16 ? 16 : lim);
-          attend_tile<D, FP8, true>(st, t, qop, scale_log2, grp, lim);
-        },
-        kc, vc, ks, vs, my_blk, r0, r1, kvh, Hkv, BS, NB, lane, col, grp);
+  const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
+  const int region = D * BS * LT::ESZ;
+  int my_blk = -1, range0 = -1;  // lane i: block id of the current 64-block range's i-th block
+
+  // Tile i's block (range-cached table read), region base and position.
+  auto tile_src = [&](int i, int64_t &rbase, int &o0, int &blk_ok, float &ksc, float &vsc) {
+    const int ts = 16 * i;
+    const int bi = ts / BS;
+    const int r = bi >> 6;
+    if (r != range0) {  // uniform: a new range of 64 blocks
+      range0 = r;
+      my_blk = -1;
+      if (r * 64 + lane < Mb) my_blk = bt[b * bt_stride + r * 64 + lane];
+    }
+    int blk = __builtin_amdgcn_readlane(my_blk, bi & 63);
+    blk_ok = (blk >= 0 && blk < NB) ? 1 : 0;
+    if (!blk_ok) blk = 0;
+    rbase = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(blk * Hkv + kvh)) * region;
+    o0 = ts % BS;
+    ksc = vsc = 1.f;
+    if constexpr (FP8) {
+      ksc = ks[static_cast<int64_t>(blk) * Hkv + kvh];
+      vsc = vs[static_cast<int64_t>(blk) * Hkv + kvh];
+    }
+  };
+
+  u32x4 stage[LT::PER_THREAD];
+  auto fetch = [&](int i, int &blk_ok, float &ksc, float &vsc) {
+    int64_t rbase;
+    int o0;
+    tile_src(i, rbase, o0, blk_ok, ksc, vsc);
+#pragma unroll
+    for (int k = 0; k < LT::PER_THREAD; ++k) {
+      const int p = threadIdx.x + k * 64 * kPrefillWaves;
+      if (LT::EVEN || p < LT::PIECES)
+        stage[k] = *reinterpret_cast<const u32x4 *>(tile_piece<D, FP8>(kc, vc, rbase, o0, BS, p));
+    }
+  };
+  auto deposit = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < LT::PER_THREAD; ++k) {
+      const int p = threadIdx.x + k * 64 * kPrefillWaves;
+      if (LT::EVEN || p < LT::PIECES) *reinterpret_cast<u32x4 *>(&lds[buf][p * 16]) = stage[k];
+    }
+  };
+
+  if (n_tiles > 0) {
+    int ok_cur, ok_next = 0;
+    float ksc_cur, vsc_cur, ksc_next = 1.f, vsc_next = 1.f;
+    fetch(0, ok_cur, ksc_cur, vsc_cur);
+    deposit(0);
+    __syncthreads();
+    for (int i = 0; i < n_tiles; ++i) {
+      const int buf = i & 1;
+      if (i + 1 < n_tiles) fetch(i + 1, ok_next, ksc_next, vsc_next);
+      if (active) {
+        Tile<D, FP8> t;
+        const uint8_t *lk = &lds[buf][0];
+        const uint8_t *lv = &lds[buf][LT::KB];
+#pragma unroll
+        for (int j = 0; j < Tile<D, FP8>::NK; ++j)
+          t.k[j] = *reinterpret_cast<const u32x4 *>(lk + ((4 * j + grp) * 16 + col) * 16);
+        if constexpr (FP8) {
+#pragma unroll
+          for (int j = 0; j < Tile<D, FP8>::NPV / 4; ++j)
+            t.v4[j] = *reinterpret_cast<const u32x4 *>(lv + (64 * j + 16 * grp + col) * 16);
+        } else {
+#pragma unroll
+          for (int n = 0; n < Tile<D, FP8>::NPV; ++n)
+            t.v[n] = *reinterpret_cast<const u32x2 *>(lv + (16 * n + col) * 32 + grp * 8);
+        }
+        const int ts = 16 * i;
+        t.ts = ts;
+        t.valid = ok_cur ? ((kend - ts) < 16 ? (kend - ts) : 16) : 0;
+        t.ksc = ksc_cur;
+        t.vsc = vsc_cur;
+        int lim = pos - ts + 1;  // keys of the tile this column sees
+        lim = lim < 0 ? 0 : (lim > 16 ? 16 : lim);
+        if (t.valid > 0) attend_tile<D, FP8, true>(st, t, qop, scale_log2, grp, lim);
+      }
+      if (i + 1 < n_tiles) {
+        // buf ^ 1 held tile i-1: every wave finished it before the last barrier
+        deposit(buf ^ 1);
+        ok_cur = ok_next;
+        ksc_cur = ksc_next;
+        vsc_cur = vsc_next;
+      }
+      __syncthreads();
+    }
   }
+  if (!valid) return;
   float l = st.l + __shfl_xor(st.l, 16, 64);
   l += __shfl_xor(l, 32, 64);
-  if (!valid) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint16_t *op = out + static_cast<int64_t>(q0 + tok) * o_st + static_cast<int64_t>(h) * o_sh;
 #pragma unroll
@@ -129,10 +253,11 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   WKV_CHECK_ARG(std::isfinite(scale), "scale must be finite");
   const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
   const int n_hg = (G + kPrefillWaves - 1) / kPrefillWaves;
-  const int64_t gy = static_cast<int64_t>(Hkv) * n_hg;
-  WKV_CHECK_ARG(gy <= 65535, "num_q_heads too large");
-  const dim3 grid(static_cast<unsigned>((max_query_len + 15) / 16), static_cast<unsigned>(gy),
-                  static_cast<unsigned>(batch));
+  const int n_qt = (max_query_len + 15) / 16;
+  const int64_t n_items = static_cast<int64_t>(batch) * Hkv * n_hg;
+  const int64_t n_wg = (n_items + 7) / 8 * 8 * n_qt;
+  WKV_CHECK_ARG(n_wg <= INT32_MAX, "prefill grid too large");
+  const dim3 grid(static_cast<unsigned>(n_wg));
   auto s = static_cast<hipStream_t>(stream);
   auto kc = static_cast<const uint8_t *>(cache->k);
   auto vc = static_cast<const uint8_t *>(cache->v);
@@ -144,7 +269,7 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   prefill_gqa_kernel<Dv, F8><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                \
       kc, vc, cache->k_scale, cache->v_scale, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h,       \
       cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS,           \
-      cache->num_blocks, scale_log2)
+      cache->num_blocks, scale_log2, n_qt, static_cast<int>(n_items))
   if (D == 128) {
     if (fp8) WKV_PREFILL(128, true); else WKV_PREFILL(128, false);
   } else {
