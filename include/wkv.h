@@ -149,7 +149,18 @@ int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stri
                          void *out, int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
                          int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
                          int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
-                         int64_t workspace_bytes, void *stream);
+                         int64_t workspace_bytes, const int32_t *seq_order, void *stream);
+
+/* seq_order (optional, NULL = batch order) for the two GQA decode calls: a
+ * permutation of 0..batch-1 in device memory giving the order in which
+ * sequences are dispatched (entries outside 0..batch-1 are skipped, leaving
+ * that output unwritten). The result does not depend on it, bit for bit;
+ * dispatching long contexts first shortens a launch over mixed lengths.
+ * wkv_decode_order writes that order -- sequence indices by seq_lens, longest
+ * first, ties by index -- into order[batch]: one call per step serves every
+ * layer. No reference counterpart (vLLM's decode launch takes sequences in
+ * batch order); an addition of this library's. */
+int wkv_decode_order(const int32_t *seq_lens, int32_t batch, int32_t *order, void *stream);
 
 /* One whole decode step of one layer in one launch: append token b of
  * key/value ([batch, num_kv_heads, head_dim] bf16) at slot_mapping[b] (-1 =
@@ -168,7 +179,8 @@ int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64
                                 int64_t q_stride_b, int64_t q_stride_h, void *out, int32_t num_q_heads,
                                 const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
                                 const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
-                                int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream);
+                                int32_t partition_size, void *workspace, int64_t workspace_bytes,
+                                const int32_t *seq_order, void *stream);
 
 /* Group-aware decode for GRPO groups (the n samples of one prompt):
  * sequences g*group_size .. g*group_size+group_size-1 form group g (the last

@@ -88,26 +88,33 @@ def test_decode_rejects_bad_arguments_before_launch():
     d = _desc()
     f = lib.wkv_paged_decode_gqa
     # Hq not a multiple of Hkv
-    assert f(ctypes.byref(d), 16, 1024, 128, 16, 3, 16, 4, 4, 16, 1, 64, 0.1, 0, None, 0, None) == _lib.WKV_ERR_INVALID
+    assert f(ctypes.byref(d), 16, 1024, 128, 16, 3, 16, 4, 4, 16, 1, 64, 0.1, 0, None, 0, None, None) == _lib.WKV_ERR_INVALID
     # group size 32 > 16 is not supported
-    assert f(ctypes.byref(d), 16, 8192, 128, 16, 64, 16, 4, 4, 16, 1, 64, 0.1, 0, None, 0, None) == _lib.WKV_ERR_UNSUPPORTED
+    assert f(ctypes.byref(d), 16, 8192, 128, 16, 64, 16, 4, 4, 16, 1, 64, 0.1, 0, None, 0, None, None) == _lib.WKV_ERR_UNSUPPORTED
     # partition not a multiple of 16
-    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, 0.1, 24, None, 0, None) == _lib.WKV_ERR_INVALID
+    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, 0.1, 24, None, 0, None, None) == _lib.WKV_ERR_INVALID
     # workspace missing when the context spans several workgroups (64 partitions of 16)
-    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 64, 64, 16, 1, 1024, 0.1, 16, None, 0, None) == _lib.WKV_ERR_INVALID
+    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 64, 64, 16, 1, 1024, 0.1, 16, None, 0, None, None) == _lib.WKV_ERR_INVALID
     assert "workspace" in _lib.last_error()
     # a partition spanning more than 64 blocks
-    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, 0.1, 2048, None, 0, None) == _lib.WKV_ERR_INVALID
+    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, 0.1, 2048, None, 0, None, None) == _lib.WKV_ERR_INVALID
     # fused append: partition must be a multiple of the block size
     g = lib.wkv_append_paged_decode_gqa
     assert g(ctypes.byref(d), 16, 256, 128, 16, 256, 128, 16, 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, 0.1, 24,
-             None, 0, None) == _lib.WKV_ERR_INVALID
+             None, 0, None, None) == _lib.WKV_ERR_INVALID
     assert g(ctypes.byref(d), None, 256, 128, 16, 256, 128, 16, 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, 0.1, 0,
-             None, 0, None) == _lib.WKV_ERR_INVALID
+             None, 0, None, None) == _lib.WKV_ERR_INVALID
     # non-finite scale
-    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, float("nan"), 0, None, 0, None) == _lib.WKV_ERR_INVALID
+    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 1, 64, float("nan"), 0, None, 0, None, None) == _lib.WKV_ERR_INVALID
     # empty batch is a no-op success
-    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 0, 64, 0.1, 0, None, 0, None) == _lib.WKV_OK
+    assert f(ctypes.byref(d), 16, 1024, 128, 16, 8, 16, 4, 4, 16, 0, 64, 0.1, 0, None, 0, None, None) == _lib.WKV_OK
+    # dispatch order: batch range and NULL pointers checked before any launch; empty batch is a no-op
+    o = lib.wkv_decode_order
+    assert o(16, -1, 16, None) == _lib.WKV_ERR_INVALID
+    assert o(16, 65536, 16, None) == _lib.WKV_ERR_INVALID
+    assert o(None, 4, 16, None) == _lib.WKV_ERR_INVALID
+    assert o(16, 4, None, None) == _lib.WKV_ERR_INVALID
+    assert o(None, 0, None, None) == _lib.WKV_OK
 
 
 @host_only

@@ -51,6 +51,27 @@ def _max_len(seq_lens: torch.Tensor, max_seq_len: int | None) -> int:
     return int(seq_lens.max().item()) if seq_lens.numel() else 0
 
 
+def decode_order(seq_lens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Dispatch order for ``paged_decode_gqa``: int32 ``[B]`` sequence indices by
+    ``seq_lens``, longest first, ties by index (computed on the device).
+
+    A decode launch lasts as long as its last workgroups; dispatching the long
+    contexts first lets the short ones fill in behind them. The order depends
+    only on the lengths, so one call per step serves every layer.
+    """
+    if seq_lens.dtype != torch.int32 or seq_lens.dim() != 1 or not seq_lens.is_contiguous():
+        raise ValueError("seq_lens must be a contiguous int32 vector")
+    batch = seq_lens.shape[0]
+    if out is None:
+        out = torch.empty(batch, dtype=torch.int32, device=seq_lens.device)
+    elif (out.dtype != torch.int32 or tuple(out.shape) != (batch,) or not out.is_contiguous()
+          or out.device != seq_lens.device):
+        raise ValueError(f"out must be a contiguous int32 [{batch}] tensor on {seq_lens.device}")
+    _lib.check(_lib.load().wkv_decode_order(seq_lens.data_ptr(), batch, out.data_ptr(), _stream(seq_lens.device)),
+               "decode_order")
+    return out
+
+
 def paged_decode_gqa(
     q: torch.Tensor,
     cache: PagedKVCache,
@@ -64,6 +85,7 @@ def paged_decode_gqa(
     new_key: torch.Tensor | None = None,
     new_value: torch.Tensor | None = None,
     slot_mapping: torch.Tensor | None = None,
+    seq_order: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One decode step of GQA attention: ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` bf16.
 
@@ -73,6 +95,9 @@ def paged_decode_gqa(
     append is fused into the same launch: token ``b`` is written at
     ``slot_mapping[b]`` (position ``seq_lens[b] - 1`` of sequence ``b``) before
     attention reads it -- the same result as ``cache.append`` then this call.
+    ``seq_order`` (int32 ``[B]``, a permutation of ``0..B-1``, e.g. from
+    ``decode_order``) sets the order in which sequences are dispatched; the
+    result is the same, bit for bit, in any order.
     """
     if not isinstance(cache, PagedKVCache):
         raise ValueError("cache must be a PagedKVCache")
@@ -97,6 +122,9 @@ def paged_decode_gqa(
         out = torch.empty((batch, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, hq, cache.head_dim) or not out.is_contiguous():
         raise ValueError("out must be a contiguous bfloat16 [B, Hq, D] tensor")
+    if seq_order is not None and (seq_order.dtype != torch.int32 or tuple(seq_order.shape) != (batch,)
+                                  or not seq_order.is_contiguous() or seq_order.device != dev):
+        raise ValueError(f"seq_order must be a contiguous int32 [{batch}] tensor on {dev}")
     if batch == 0:
         return out
     lib = _lib.load()
@@ -107,7 +135,8 @@ def paged_decode_gqa(
     ws = _workspace(dev, need)
     tail = (q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq, block_table.data_ptr(),
             block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl, float(scale),
-            int(partition_size), ws.data_ptr(), ws.numel(), _stream(dev))
+            int(partition_size), ws.data_ptr(), ws.numel(),
+            seq_order.data_ptr() if seq_order is not None else None, _stream(dev))
     if fused:
         rc = lib.wkv_append_paged_decode_gqa(
             ctypes.byref(cache.descriptor()), new_key.data_ptr(), new_key.stride(0), new_key.stride(1),

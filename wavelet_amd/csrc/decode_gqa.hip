@@ -31,7 +31,7 @@ __device__ __forceinline__ int balanced_partition(int n, int W, int P_tok, int u
   return __builtin_amdgcn_readfirstlane(p);
 }
 
-// Grid: (chunk, KV head, sequence); W waves per workgroup, wave w of chunk c
+// Grid: (chunk, KV head, sequence or dispatch rank); W waves per workgroup, wave w of chunk c
 // owns partition c*W + w of P_tok tokens. The waves of a workgroup merge
 // their partials through LDS; a context longer than one chunk leaves one
 // partial per chunk for merge_partials_kernel.
@@ -40,9 +40,9 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ ks, float *__restrict__ vs,
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ out,
     float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
-    int Mb, int max_seq, const int32_t *__restrict__ seq_lens, int Hq, int Hkv, int G, int BS, int64_t NB,
-    float scale_log2, int P_tok, int max_chunks, StepAppend ap) {
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    int Mb, int max_seq, const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ order, int Hq, int Hkv,
+    int G, int BS, int64_t NB, float scale_log2, int P_tok, int max_chunks, StepAppend ap) {
+  const int chunk = blockIdx.x, kvh = blockIdx.y;
   // The wave index is uniform across the wave; saying so keeps everything
   // derived from it (partition, block ids, buffer resources) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -51,6 +51,12 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
   int t_begin = part * P_tok;
   int blk_first = t_begin / BS;
 
+  // Sequence: blockIdx.z, or the z-th entry of a dispatch order (longest
+  // contexts first: the short ones then fill the gaps the long ones leave).
+  // The loads of sequence blockIdx.z go out while the order entry is read
+  // and are redone only when the entry names another sequence.
+  int b = blockIdx.z;
+  const int b_ord = order != nullptr ? order[b] : b;
   // Loads that do not depend on the context length go out together with it:
   // the block ids of a full-size partition (bounded by the block-table width) and q.
   int L = seq_lens[b];
@@ -59,6 +65,14 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
   // Q^T operand: lane holds 8 d-values of head `col` (zero for padded heads).
   bf16x8 qop[D / 32];
   load_q<D, FP8>(qop, q + b * q_sb + static_cast<int64_t>(kvh * G + (col < G ? col : 0)) * q_sh, col < G, grp);
+  if (b_ord != b) {
+    if (b_ord < 0 || b_ord >= static_cast<int>(gridDim.z)) return;  // not an entry of a permutation of the batch
+    b = b_ord;
+    L = seq_lens[b];
+    my_blk = -1;
+    if (blk_first + lane < Mb) my_blk = bt[b * bt_stride + blk_first + lane];
+    load_q<D, FP8>(qop, q + b * q_sb + static_cast<int64_t>(kvh * G + (col < G ? col : 0)) * q_sh, col < G, grp);
+  }
 
   L = L < max_seq ? L : max_seq;  // max_seq <= block-table width * BS: every read stays in the table
   if (L <= 0) {
@@ -588,11 +602,34 @@ extern "C" int64_t wkv_decode_workspace_size(int32_t batch, int32_t num_q_heads,
 
 namespace wkv {
 
+// Dispatch order for the decode kernels: the batch's sequence indices by
+// context length, longest first, ties by index -- rank(i) = #{j : L_j > L_i,
+// or L_j = L_i and j < i} is a permutation. O(batch^2) compares, spread over
+// ceil(batch / 256) workgroups (64 sequences: one 64-compare loop per thread).
+__global__ __launch_bounds__(256) void decode_order_kernel(const int32_t *__restrict__ seq_lens, int batch,
+                                                           int32_t *__restrict__ order) {
+  __shared__ int keys[256];
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int ki = i < batch ? seq_lens[i] : 0;
+  int rank = 0;
+  for (int j0 = 0; j0 < batch; j0 += 256) {
+    __syncthreads();  // the previous slice has been read by every thread
+    keys[threadIdx.x] = j0 + static_cast<int>(threadIdx.x) < batch ? seq_lens[j0 + threadIdx.x] : 0;
+    __syncthreads();
+    const int n = batch - j0 < 256 ? batch - j0 : 256;
+    for (int j = 0; j < n; ++j) {
+      const int kj = keys[j];
+      rank += (kj > ki || (kj == ki && j0 + j < i)) ? 1 : 0;
+    }
+  }
+  if (i < batch) order[rank] = i;
+}
+
 static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stride_b, int64_t q_stride_h, void *out,
                          int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
                          int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
                          float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
-                         const StepAppend *ap, void *stream) {
+                         const StepAppend *ap, const int32_t *seq_order, void *stream) {
   int rc = check_cache(cache, -1);
   if (rc) return rc;
   WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
@@ -647,7 +684,7 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   decode_gqa_kernel<Dv, F8, AP, Wv><<<grid, 64 * Wv, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, qq,       \
                                                              q_stride_b, q_stride_h, oo, part_o, part_ml,      \
                                                              block_table, bt_stride, max_blocks_per_seq,       \
-                                                             max_seq, seq_lens,                                \
+                                                             max_seq, seq_lens, seq_order,                     \
                                                              num_q_heads, Hkv, G, BS, cache->num_blocks,       \
                                                              scale_log2, partition_size, max_chunks, apv)
 #define WKV_DECODE_W(Dv, F8, AP)   \
@@ -846,14 +883,24 @@ extern "C" int wkv_paged_decode_gqa_grouped(const wkv_cache_t *cache, const void
                         max_prefix_len, scale, partition_size, workspace, workspace_bytes, stream);
 }
 
+extern "C" int wkv_decode_order(const int32_t *seq_lens, int32_t batch, int32_t *order, void *stream) {
+  WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
+  if (batch == 0) return WKV_OK;
+  WKV_CHECK_ARG(seq_lens != nullptr && order != nullptr, "seq_lens / order is NULL");
+  decode_order_kernel<<<(batch + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(seq_lens, batch, order);
+  WKV_CHECK_LAUNCH("decode order");
+  return WKV_OK;
+}
+
 extern "C" int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stride_b,
                                     int64_t q_stride_h, void *out, int32_t num_q_heads,
                                     const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
                                     const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
-                                    int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream) {
+                                    int32_t partition_size, void *workspace, int64_t workspace_bytes,
+                                    const int32_t *seq_order, void *stream) {
   return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
                        max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
-                       workspace_bytes, nullptr, stream);
+                       workspace_bytes, nullptr, seq_order, stream);
 }
 
 extern "C" int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
@@ -863,7 +910,8 @@ extern "C" int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void 
                                            const int32_t *block_table, int64_t bt_stride,
                                            int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
                                            int32_t max_seq_len, float scale, int32_t partition_size,
-                                           void *workspace, int64_t workspace_bytes, void *stream) {
+                                           void *workspace, int64_t workspace_bytes, const int32_t *seq_order,
+                                           void *stream) {
   WKV_CHECK_ARG(key && value && aligned16(key) && aligned16(value), "key/value must be non-NULL and 16-byte aligned");
   WKV_CHECK_ARG(key_stride_t >= 0 && key_stride_h >= 0 && value_stride_t >= 0 && value_stride_h >= 0 &&
                     (key_stride_t | key_stride_h | value_stride_t | value_stride_h) % 8 == 0,
@@ -875,5 +923,5 @@ extern "C" int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void 
                       static_cast<const uint16_t *>(value), value_stride_t, value_stride_h, slot_mapping};
   return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
                        max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
-                       workspace_bytes, &ap, stream);
+                       workspace_bytes, &ap, seq_order, stream);
 }

@@ -21,6 +21,11 @@ from .attention import _workspace
 from .cache import PagedKVCache, check_tables
 
 
+# Smallest B * Hkv * max_seq_len (token-heads) for which DecodeStep orders
+# its dispatch by default.
+ORDER_MIN_WORK = 1 << 20
+
+
 @dataclass
 class _LayerCall:
     append_fn: object
@@ -42,13 +47,23 @@ class DecodeStep:
     the attention is the group-aware one (``paged_decode_gqa_grouped``): GRPO
     groups of ``group_size`` consecutive sequences read their shared prompt
     blocks once per group; ``max_prefix_len`` bounds ``prefix_lens``.
+
+    Otherwise, with ``order_by_length``, ``run`` first computes the step's
+    dispatch order (``decode_order``: longest contexts first, one launch shared
+    by every layer) and each layer's decode dispatches its sequences in that
+    order; the results are the same bit for bit. ``None`` (the default) orders
+    when ``B * Hkv * max_seq_len >= 2**20``: below that a launch is short
+    enough (~50 us) that the order's dependent read at each workgroup's start
+    costs more than mixed lengths lose. Calling ``step_layer`` / ``attend``
+    directly uses the order of the last ``prepare`` (the batch order before
+    the first).
     """
 
     def __init__(self, caches: list[PagedKVCache], q: list[torch.Tensor], key: list[torch.Tensor],
                  value: list[torch.Tensor], out: list[torch.Tensor], block_table: torch.Tensor,
                  seq_lens: torch.Tensor, slot_mapping: torch.Tensor, scale: float, max_seq_len: int,
                  partition_size: int = 0, *, group_size: int = 0, prefix_lens: torch.Tensor | None = None,
-                 max_prefix_len: int = 0) -> None:
+                 max_prefix_len: int = 0, order_by_length: bool | None = None) -> None:
         if not caches:
             raise ValueError("no layers")
         dev = caches[0].device
@@ -76,6 +91,12 @@ class DecodeStep:
         self.workspace = _workspace(dev, need)
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.lib = lib
+        if order_by_length is None:
+            order_by_length = batch * c0.num_kv_heads * max_seq_len >= ORDER_MIN_WORK
+        self.ordered = bool(order_by_length) and not self.grouped
+        # always a permutation of the batch: the identity until prepare() runs
+        self.order = torch.arange(batch, dtype=torch.int32, device=dev)
+        order_ptr = self.order.data_ptr() if self.ordered else None
         self.calls: list[_LayerCall] = []
         for layer, cache in enumerate(caches):
             qq, kk, vv, oo = q[layer], key[layer], value[layer], out[layer]
@@ -98,11 +119,20 @@ class DecodeStep:
                 fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
                               vv.stride(1), slot_mapping.data_ptr(), *gtail)
             else:
+                tail = (*tail[:-1], order_ptr, tail[-1])
                 decode_args = (desc, *tail)
                 fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
                               vv.stride(1), slot_mapping.data_ptr(), *tail)
             self.calls.append(_LayerCall(fn, append_args, decode_args, fused_args))
         self._keep = (caches, q, key, value, out)
+
+    def prepare(self) -> None:
+        """Compute this step's dispatch order from ``seq_lens`` (one launch)."""
+        if self.ordered:
+            rc = self.lib.wkv_decode_order(self.seq_lens.data_ptr(), self.seq_lens.shape[0], self.order.data_ptr(),
+                                           self.stream)
+            if rc:
+                _lib.check(rc, "decode order")
 
     def append(self, layer: int) -> None:
         c = self.calls[layer]
@@ -125,6 +155,7 @@ class DecodeStep:
 
     def run(self, fused: bool = True) -> None:
         """One decode step over every layer (fused append + attention by default)."""
+        self.prepare()
         for layer in range(len(self.calls)):
             if fused:
                 self.step_layer(layer)
