@@ -74,6 +74,26 @@ def test_append_then_gather_bf16_32_seqs_bit_exact(cuda):
     assert not np.any(ok == 0xFFFF)
 
 
+@pytest.mark.parametrize("H,D,BS,T", [(8, 128, 16, 1000), (2, 64, 64, 777), (4, 128, 32, 256), (3, 64, 16, 300),
+                                       (8, 128, 16, 255)])
+def test_append_bf16_many_tokens_shuffled_slots_bit_exact(cuda, H, D, BS, T):
+    """Prompt-sized appends (the transposing kernel from 256 tokens on, the per-chunk one below):
+    slots in random order across blocks, every 7th token skipped (-1), a ragged last window,
+    key/value as strided views of a fused buffer; untouched slots keep their poison."""
+    NB = (2 * T + BS - 1) // BS
+    rng = np.random.default_rng(T * 31 + D)
+    slots = rng.permutation(NB * BS)[:T].astype(np.int64)
+    slots[::7] = -1
+    kc, vc = paged.empty_cache(NB, BS, H, D, fill=0xFFFF)
+    cache = PagedKVCache(NB, BS, H, D, device=cuda)
+    _upload(cache, kc, vc)
+    qkv = synth.normal_bf16(synth.stream_key("bulk", str(T), str(D)), (T, 3 * H, D))
+    paged.append_bf16(kc, vc, qkv[:, H:2 * H], qkv[:, 2 * H:], slots)
+    d = to_dev_bits(qkv, BF16, cuda)
+    cache.append(d[:, H:2 * H], d[:, 2 * H:], torch.from_numpy(slots).to(cuda))
+    _assert_cache_equal(cache, kc, vc, what=f"bulk append T={T}")
+
+
 def _exhaustive_bf16_rows(h: int, d: int) -> np.ndarray:
     """All 65,536 bf16 patterns sorted by magnitude (NaN last), as [tokens, h, d]."""
     bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)

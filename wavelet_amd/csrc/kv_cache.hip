@@ -40,6 +40,65 @@ __global__ __launch_bounds__(256) void append_bf16_kernel(uint16_t *__restrict__
   for (int j = 0; j < 8; ++j) vdst[j * BS] = static_cast<uint16_t>(vv[j >> 1] >> (16 * (j & 1)));
 }
 
+// bf16 append of many tokens (a prompt): workgroup = 64 consecutive tokens x
+// one head. Rows are read whole (16 bytes per thread, coalesced) into LDS,
+// transposed, and written with lanes along tokens: thread i always owns token
+// i % 64 (its slot loaded once), so one K store instruction writes 64 tokens'
+// 16-byte pieces of one chunk and one V store 64 tokens' values of one d row --
+// contiguous runs of the cache's [.., BS, 8] / [.., D, BS] rows wherever the
+// slots are consecutive, instead of 2-byte writes to 64 different rows.
+constexpr int kBulkTokens = 64;
+constexpr int64_t kBulkMinTokens = 256;  // below this (a decode step's tokens) the per-chunk kernel spreads wider
+
+template <int D>
+__global__ __launch_bounds__(256) void append_bf16_bulk_kernel(uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+                                                               const uint16_t *__restrict__ key, int64_t kst,
+                                                               int64_t ksh, const uint16_t *__restrict__ val,
+                                                               int64_t vst, int64_t vsh,
+                                                               const int64_t *__restrict__ slots, int64_t T, int H,
+                                                               int BS, int64_t NB) {
+  constexpr int C = D / 8;
+  constexpr int KP = kBulkTokens + 1;      // K pitch in 16-byte pieces: chunk rows land 4 banks apart
+  constexpr int VP = kBulkTokens * 2 + 4;  // V pitch in bytes (2-way conflicts at most on the transposing write)
+  __shared__ __attribute__((aligned(16))) u32x4 lk[C * KP];
+  __shared__ __attribute__((aligned(16))) uint8_t lv[D * VP];
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kBulkTokens;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x;
+  // load: thread -> (token tid / C + k * (256 / C), chunk tid % C)
+  {
+    const int c = tid % C;
+#pragma unroll
+    for (int k = 0; k < kBulkTokens * C / 256; ++k) {
+      const int t = tid / C + k * (256 / C);
+      if (t0 + t < T) {
+        const u32x4 kv = *reinterpret_cast<const u32x4 *>(key + (t0 + t) * kst + h * ksh + c * 8);
+        const u32x4 vv = *reinterpret_cast<const u32x4 *>(val + (t0 + t) * vst + h * vsh + c * 8);
+        lk[c * KP + t] = kv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<uint16_t *>(&lv[(c * 8 + j) * VP + t * 2]) =
+              static_cast<uint16_t>(vv[j >> 1] >> (16 * (j & 1)));
+      }
+    }
+  }
+  __syncthreads();
+  const int t = tid % kBulkTokens;
+  if (t0 + t >= T) return;
+  const int64_t slot = slots[t0 + t];
+  if (slot < 0) return;
+  const int64_t blk = slot / BS;
+  const int off = static_cast<int>(slot % BS);
+  if (blk >= NB) return;  // out-of-range ids are never written (no fault)
+  const int r0 = tid / kBulkTokens;  // 0..3
+  uint16_t *kdst = kc + ((blk * H + h) * C * BS + off) * 8;
+#pragma unroll
+  for (int c = r0; c < C; c += 4) *reinterpret_cast<u32x4 *>(kdst + static_cast<int64_t>(c) * BS * 8) = lk[c * KP + t];
+  uint16_t *vdst = vc + (blk * H + h) * D * BS + off;
+#pragma unroll 8
+  for (int d = r0; d < D; d += 4) vdst[static_cast<int64_t>(d) * BS] = *reinterpret_cast<const uint16_t *>(&lv[d * VP + t * 2]);
+}
+
 template <int D>
 __global__ __launch_bounds__(64) void append_fp8_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
                                                         float *__restrict__ ks, float *__restrict__ vs,
@@ -219,7 +278,18 @@ extern "C" int wkv_append(const wkv_cache_t *cache, const void *key, int64_t key
   auto vc = static_cast<uint16_t *>(cache->v);
   auto k = static_cast<const uint16_t *>(key);
   auto v = static_cast<const uint16_t *>(value);
-  if (D == 128)
+  if (num_tokens >= kBulkMinTokens) {  // a prompt: the transposing kernel
+    WKV_CHECK_ARG(H <= 65535, "num_kv_heads too large");
+    const dim3 bgrid(static_cast<unsigned>((num_tokens + kBulkTokens - 1) / kBulkTokens), static_cast<unsigned>(H));
+    if (D == 128)
+      append_bf16_bulk_kernel<128><<<bgrid, 256, 0, s>>>(kc, vc, k, key_stride_t, key_stride_h, v, value_stride_t,
+                                                         value_stride_h, slot_mapping, num_tokens, H,
+                                                         cache->block_size, cache->num_blocks);
+    else
+      append_bf16_bulk_kernel<64><<<bgrid, 256, 0, s>>>(kc, vc, k, key_stride_t, key_stride_h, v, value_stride_t,
+                                                        value_stride_h, slot_mapping, num_tokens, H,
+                                                        cache->block_size, cache->num_blocks);
+  } else if (D == 128)
     append_bf16_kernel<128><<<grid, 256, 0, s>>>(kc, vc, k, key_stride_t, key_stride_h, v, value_stride_t,
                                                  value_stride_h, slot_mapping, num_tokens, H, cache->block_size,
                                                  cache->num_blocks);
