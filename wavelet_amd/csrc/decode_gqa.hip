@@ -660,8 +660,10 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
                   partition_size, BS);
   const int max_parts = max_seq > 0 ? (max_seq + partition_size - 1) / partition_size : 1;
   // Waves per workgroup: partitions of one context share a workgroup (and an
-  // LDS merge) up to 4 at a time; longer contexts leave per-chunk partials.
-  const int W = max_parts <= 1 ? 1 : (max_parts <= 2 ? 2 : 4);
+  // LDS merge) up to 8 at a time; longer contexts leave per-chunk partials.
+  // (8-wave workgroups for 8+ partitions: var-length Qwen3-4B -7%, Qwen2.5-0.5B
+  // -11% against 4; the 4-partition headline shape stays at 4.)
+  const int W = max_parts <= 1 ? 1 : (max_parts <= 2 ? 2 : (max_parts < 8 ? 4 : 8));
   const int max_chunks = (max_parts + W - 1) / W;
   WKV_CHECK_ARG(max_chunks <= 65535, "too many partitions (%d)", max_parts);
   const int64_t need = wkv_decode_workspace_size(batch, num_q_heads, D, max_seq, partition_size * W);
@@ -693,8 +695,10 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
       WKV_DECODE(Dv, F8, AP, 1);   \
     else if (W == 2)               \
       WKV_DECODE(Dv, F8, AP, 2);   \
-    else                           \
+    else if (W == 4)               \
       WKV_DECODE(Dv, F8, AP, 4);   \
+    else                           \
+      WKV_DECODE(Dv, F8, AP, 8);   \
   } while (0)
   if (D == 128) {
     if (fp8) { if (ap) WKV_DECODE_W(128, true, true); else WKV_DECODE_W(128, true, false); }
