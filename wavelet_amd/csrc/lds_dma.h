@@ -1,0 +1,41 @@
+// LDS-DMA helpers for gfx950: HBM -> LDS copies without register staging
+// (global_load_lds_dwordx4: lane i of a wave instruction lands at the LDS
+// address in M0 + 16 i), the waits for them, and an LDS barrier.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace wkv {
+
+// The copies, the waits for them and the barriers are written as inline asm
+// so the compiler's own wait-count insertion never sees an LDS write it would
+// have to wait for: it cannot always prove that a read of one step buffer
+// does not alias the copies still landing in the others, and then waits for
+// every outstanding copy (vmcnt(0)), which would drain the pipeline. The
+// "memory" clobbers keep the compiler from moving LDS accesses across them.
+// M0 carries the LDS address of an LDS-DMA copy; nothing else in the kernel
+// uses M0, and each copy sets it immediately before use.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void copy16_to_lds(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Waits until at most N of this wave's vector-memory operations are pending.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier for LDS: this wave's LDS accesses complete, then s_barrier.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p));
+}
+
+}  // namespace wkv

@@ -15,22 +15,26 @@
 // one XCD (the dispatcher deals workgroup i to XCD i mod 8): the keys are
 // served from that XCD's L2 instead of being fetched by all eight. The
 // latest (most expensive, causally) query tiles are dispatched first.
-// Keys are streamed in 16-token tiles staged once per workgroup in LDS (double
-// buffered: every thread fetches its 16-byte pieces of tile i+1 while the
-// waves attend tile i from LDS with the decode kernels' tile arithmetic,
-// gqa_tiles.h); tiles on the causal diagonal mask per lane (column). Every
-// wave finishes its rows: no split-K, no workspace.
+// Keys are streamed in 16-token tiles copied once per workgroup into LDS by
+// LDS-DMA (three buffers: two tiles in flight while the waves attend the
+// third with the decode kernels' tile arithmetic, gqa_tiles.h); tiles on the
+// causal diagonal mask per lane (column). Every wave finishes its rows: no
+// split-K, no workspace.
 #include "gqa_tiles.h"
+#include "lds_dma.h"
 
 namespace wkv {
 
 constexpr int kPrefillWaves = 4;
 
-// One 16-token key tile of one (block, KV head) in LDS, in the cache's order:
-// K as [D/x chunks][16 tokens][16 bytes], V as [D rows][16 tokens x element].
-// A lane's MFMA operand is then one contiguous LDS read (K: 16 bytes of chunk
-// 4j+grp, token col; V: bf16 tokens 4grp..4grp+3 of row 16n+col, fp8 the
-// whole row 64j+16grp+col), and a wave's reads cover contiguous bytes.
+// One 16-token key tile of one (block, KV head) in LDS: K as the cache holds
+// it, [D/x chunks][16 tokens][16 bytes]; fp8 V as the cache holds it, [D rows]
+// [16 tokens]; bf16 V as [2 token octets][D rows][8 tokens] (16-byte pieces,
+// so the copy still moves whole pieces). A lane's MFMA operand is one LDS read
+// (K: 16 bytes of chunk 4j+grp, token col; bf16 V: tokens 4grp..4grp+3 of row
+// 16n+col, 8 bytes at a 16-byte stride across the lanes -- at the cache's
+// 32-byte row stride those reads conflicted on the LDS banks; fp8 V: the whole
+// row 64j+16grp+col).
 template <int D, bool FP8>
 struct LdsTile {
   static constexpr int ESZ = FP8 ? 1 : 2;
@@ -40,6 +44,9 @@ struct LdsTile {
   static constexpr int PIECES = BYTES / 16;  // 16-byte pieces
   static constexpr int PER_THREAD = (PIECES + 64 * kPrefillWaves - 1) / (64 * kPrefillWaves);
   static constexpr bool EVEN = PIECES % (64 * kPrefillWaves) == 0;  // else the last round is partial
+  // A wave issues PER_THREAD copies per tile, or none (its waits count on it).
+  static_assert(EVEN || PIECES < 64 * kPrefillWaves, "copies per wave: PER_THREAD or 0");
+  static_assert(PIECES % 64 == 0, "whole wave instructions");
 };
 
 // Global address of 16-byte piece p of the tile (tokens o0..o0+15 of block
@@ -52,12 +59,14 @@ __device__ __forceinline__ const uint8_t *tile_piece(const uint8_t *kc, const ui
     const int c = p >> 4, m = p & 15;
     return kc + rbase + (static_cast<int64_t>(c) * BS + o0 + m) * 16;
   }
-  // V row d: the 16 tokens are 32 (bf16) or 16 (fp8) contiguous bytes
+  // V row d: the 16 tokens are 32 (bf16) or 16 (fp8) contiguous bytes;
+  // bf16 piece v holds octet v / D of row v % D
   const int v = p - T::KB / 16;
-  constexpr int PPR = 16 * T::ESZ / 16;  // pieces per row
-  const int d = v / PPR, half = v % PPR;
+  const int d = FP8 ? v : v % D, half = FP8 ? 0 : v / D;
   return vc + rbase + (static_cast<int64_t>(d) * BS + o0) * T::ESZ + half * 16;
 }
+
+constexpr int kPrefillBufs = 3;  // LDS tile buffers: one attended, two in flight
 
 template <int D, bool FP8>
 __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
@@ -67,7 +76,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
     const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
     int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
   using LT = LdsTile<D, FP8>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][LT::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kPrefillBufs][LT::BYTES];
   // Linear id = ((item / 8) * n_qt + (n_qt - 1 - qt)) * 8 + item % 8, item =
   // (sequence, KV head, head group): the XCD (id % 8) depends on the item only.
   const int id = blockIdx.x;
@@ -107,19 +116,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
   const int kend = ctx + last + 1;
   const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
   const int region = D * BS * LT::ESZ;
-  int my_blk = -1, range0 = -1;  // lane i: block id of the current 64-block range's i-th block
-
-  // Tile i's block (range-cached table read), region base and position.
+  // Tile i's block (a wave-uniform table read: a scalar load, which waits on
+  // its own counter and never on the tile copies in flight), region base and
+  // position.
   auto tile_src = [&](int i, int64_t &rbase, int &o0, int &blk_ok, float &ksc, float &vsc) {
     const int ts = 16 * i;
     const int bi = ts / BS;
-    const int r = bi >> 6;
-    if (r != range0) {  // uniform: a new range of 64 blocks
-      range0 = r;
-      my_blk = -1;
-      if (r * 64 + lane < Mb) my_blk = bt[b * bt_stride + r * 64 + lane];
-    }
-    int blk = __builtin_amdgcn_readlane(my_blk, bi & 63);
+    int blk = bi < Mb ? bt[b * bt_stride + bi] : -1;
     blk_ok = (blk >= 0 && blk < NB) ? 1 : 0;
     if (!blk_ok) blk = 0;
     rbase = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(blk * Hkv + kvh)) * region;
@@ -131,68 +134,74 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
     }
   };
 
-  u32x4 stage[LT::PER_THREAD];
-  auto fetch = [&](int i, int &blk_ok, float &ksc, float &vsc) {
+  // Tiles are copied HBM -> LDS by LDS-DMA (no register staging): wave w's
+  // k-th copy moves pieces 256 k + 64 w .. + 63, lane i piece 256 k + 64 w + i,
+  // to LDS offset 16 * piece. Tile i + 2 is issued at the start of iteration i
+  // into the buffer tile i - 1 left; before the barrier that publishes tile
+  // i + 1 each wave waits for its own copies of it.
+  const int wave_base = 64 * wave;
+  int okr[kPrefillBufs];
+  float kscr[kPrefillBufs], vscr[kPrefillBufs];
+  auto issue = [&](int i, int bi) {
     int64_t rbase;
     int o0;
-    tile_src(i, rbase, o0, blk_ok, ksc, vsc);
+    tile_src(i, rbase, o0, okr[bi], kscr[bi], vscr[bi]);
+    const uint32_t dst = lds_addr(&lds[bi][0]);
 #pragma unroll
     for (int k = 0; k < LT::PER_THREAD; ++k) {
-      const int p = threadIdx.x + k * 64 * kPrefillWaves;
-      if (LT::EVEN || p < LT::PIECES)
-        stage[k] = *reinterpret_cast<const u32x4 *>(tile_piece<D, FP8>(kc, vc, rbase, o0, BS, p));
+      const int p0 = 256 * k + wave_base;  // uniform: this wave instruction's first piece
+      if (LT::EVEN || p0 < LT::PIECES)
+        copy16_to_lds(tile_piece<D, FP8>(kc, vc, rbase, o0, BS, p0 + lane),
+                      __builtin_amdgcn_readfirstlane(dst + 16 * p0));
     }
   };
-  auto deposit = [&](int buf) {
+  auto attend = [&](int i, int bi) {
+    Tile<D, FP8> t;
+    const uint8_t *lk = &lds[bi][0];
+    const uint8_t *lv = &lds[bi][LT::KB];
 #pragma unroll
-    for (int k = 0; k < LT::PER_THREAD; ++k) {
-      const int p = threadIdx.x + k * 64 * kPrefillWaves;
-      if (LT::EVEN || p < LT::PIECES) *reinterpret_cast<u32x4 *>(&lds[buf][p * 16]) = stage[k];
+    for (int j = 0; j < Tile<D, FP8>::NK; ++j)
+      t.k[j] = *reinterpret_cast<const u32x4 *>(lk + ((4 * j + grp) * 16 + col) * 16);
+    if constexpr (FP8) {
+#pragma unroll
+      for (int j = 0; j < Tile<D, FP8>::NPV / 4; ++j)
+        t.v4[j] = *reinterpret_cast<const u32x4 *>(lv + (64 * j + 16 * grp + col) * 16);
+    } else {
+#pragma unroll
+      for (int n = 0; n < Tile<D, FP8>::NPV; ++n)
+        t.v[n] = *reinterpret_cast<const u32x2 *>(lv + ((grp >> 1) * D + 16 * n + col) * 16 + (grp & 1) * 8);
     }
+    const int ts = 16 * i;
+    t.ts = ts;
+    t.valid = okr[bi] ? ((kend - ts) < 16 ? (kend - ts) : 16) : 0;
+    t.ksc = kscr[bi];
+    t.vsc = vscr[bi];
+    int lim = pos - ts + 1;  // keys of the tile this column sees
+    lim = lim < 0 ? 0 : (lim > 16 ? 16 : lim);
+    if (t.valid > 0) attend_tile<D, FP8, true>(st, t, qop, scale_log2, grp, lim);
   };
 
   if (n_tiles > 0) {
-    int ok_cur, ok_next = 0;
-    float ksc_cur, vsc_cur, ksc_next = 1.f, vsc_next = 1.f;
-    fetch(0, ok_cur, ksc_cur, vsc_cur);
-    deposit(0);
-    __syncthreads();
+    issue(0, 0);
+    if (n_tiles > 1) {
+      issue(1, 1);
+      wait_vmcnt<LT::PER_THREAD>();  // tile 0 landed
+    } else {
+      wait_vmcnt<0>();
+    }
+    barrier_lds();
+    int bi = 0;  // buffer of tile i
     for (int i = 0; i < n_tiles; ++i) {
-      const int buf = i & 1;
-      if (i + 1 < n_tiles) fetch(i + 1, ok_next, ksc_next, vsc_next);
-      if (active) {
-        Tile<D, FP8> t;
-        const uint8_t *lk = &lds[buf][0];
-        const uint8_t *lv = &lds[buf][LT::KB];
-#pragma unroll
-        for (int j = 0; j < Tile<D, FP8>::NK; ++j)
-          t.k[j] = *reinterpret_cast<const u32x4 *>(lk + ((4 * j + grp) * 16 + col) * 16);
-        if constexpr (FP8) {
-#pragma unroll
-          for (int j = 0; j < Tile<D, FP8>::NPV / 4; ++j)
-            t.v4[j] = *reinterpret_cast<const u32x4 *>(lv + (64 * j + 16 * grp + col) * 16);
-        } else {
-#pragma unroll
-          for (int n = 0; n < Tile<D, FP8>::NPV; ++n)
-            t.v[n] = *reinterpret_cast<const u32x2 *>(lv + (16 * n + col) * 32 + grp * 8);
-        }
-        const int ts = 16 * i;
-        t.ts = ts;
-        t.valid = ok_cur ? ((kend - ts) < 16 ? (kend - ts) : 16) : 0;
-        t.ksc = ksc_cur;
-        t.vsc = vsc_cur;
-        int lim = pos - ts + 1;  // keys of the tile this column sees
-        lim = lim < 0 ? 0 : (lim > 16 ? 16 : lim);
-        if (t.valid > 0) attend_tile<D, FP8, true>(st, t, qop, scale_log2, grp, lim);
-      }
-      if (i + 1 < n_tiles) {
-        // buf ^ 1 held tile i-1: every wave finished it before the last barrier
-        deposit(buf ^ 1);
-        ok_cur = ok_next;
-        ksc_cur = ksc_next;
-        vsc_cur = vsc_next;
-      }
-      __syncthreads();
+      const int b2 = bi == 0 ? 2 : bi - 1;  // (i + 2) mod 3: the buffer tile i - 1 left
+      const bool more = i + 2 < n_tiles;
+      if (more) issue(i + 2, b2);
+      if (active) attend(i, bi);
+      if (more)
+        wait_vmcnt<LT::PER_THREAD>();  // tile i + 1 landed, tile i + 2 may be in flight
+      else
+        wait_vmcnt<0>();
+      barrier_lds();  // tile i + 1 visible; every wave is done with tile i
+      bi = bi == 2 ? 0 : bi + 1;
     }
   }
   if (!valid) return;
