@@ -312,8 +312,6 @@ def workload(args, torch, dev) -> dict:
                 self.n += 1
                 sample(logits, temperature=0.7, top_k=50, top_p=0.9, seeds=seeds, step=self.n, return_mask=True)
 
-            attend = append = step_layer
-
             def run(self):
                 self.step_layer(0)
 
@@ -322,7 +320,7 @@ def workload(args, torch, dev) -> dict:
                                        context_lens=np.ones(B))
         words = (V + 31) // 32
         nbytes = B * V * 2 + B * (8 + 4 + 4) + B * words * 4
-        return {"name": name, "step": _Step(), "w": w, "layer_bytes": nbytes, "attn_bytes": nbytes,
+        return {"name": name, "step": _Step(), "w": w, "layer_bytes": nbytes, "attn_bytes": nbytes, "split": False,
                 "kernel": "sample_kernel<bf16>", "dtype": "bf16 logits, fp32 math", "flops_per_layer": 0,
                 "metric": "sampler GB/s of logits & us/step, 256 x 151936",
                 "cache_bytes": B * V * 2,
@@ -397,8 +395,9 @@ def main() -> int:
         return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3
 
     kernel_us = per_launch(step.step_layer, args.kernel_reps)
-    attend_us = per_launch(step.attend, 1)
-    append_us = per_launch(step.append, 1)
+    split = wl.get("split", True)  # the step has separate append and attention calls
+    attend_us = per_launch(step.attend, 1) if split else None
+    append_us = per_launch(step.append, 1) if split else None
     ceiling = copy_ceiling_gbs(torch, dev)
 
     step_bytes = wl["layer_bytes"] * args.layers
@@ -462,9 +461,10 @@ def main() -> int:
             "mean_launch_us": round(kernel_us, 2),
             "tflops": round(wl["flops_per_layer"] / (kernel_us * 1e-6) / 1e12, 2),
         },
-        "unfused_us": {"append": round(append_us, 2), "attention": round(attend_us, 2)},
         "hbm_copy_gbs": round(ceiling, 1),
     }
+    if split:
+        rec["unfused_us"] = {"append": round(append_us, 2), "attention": round(attend_us, 2)}
     if "logical_kv_bytes" in wl and wl["w"].group_size > 1:
         rec["config"]["logical_kv_bytes_per_layer"] = wl["logical_kv_bytes"]
     if headline and not args.no_cpu_baseline:
