@@ -19,23 +19,17 @@ ROWS = [(1.0, 0, 1.0, 0.0, 1.0), (0.7, 50, 1.0, 0.0, 1.0), (1.0, 0, 0.9, 0.0, 1.
         (0.8, 40, 0.8, 0.01, 1.3), (0.0, 0, 1.0, 0.0, 1.0), (1.0, 1, 1.0, 0.0, 1.0), (0.6, 0, 0.3, 0.0, 1.1)]
 
 
-@pytest.mark.parametrize("vocab", [151936, 32001, 1000])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_sampler_matches_oracle(cuda, vocab, dtype):
-    B = len(ROWS)
-    x = (synth.normal(synth.stream_key("smp", vocab, str(dtype)), B * vocab) * 4.0).astype(np.float32).reshape(B, vocab)
+def _check_rows(cuda, x, rows, seen_lists, seeds, step, dtype):
+    """Run `sample` on float32 logits x [B, V] (as dtype) and compare every row with the oracle."""
+    B, vocab = x.shape
     if dtype == torch.bfloat16:
         bits = paged.f32_to_bf16(x)
         x = paged.bf16_to_f32(bits)
         logits = torch.from_numpy(bits.view(np.int16)).to(cuda).view(torch.bfloat16)
     else:
         logits = torch.from_numpy(x).to(cuda)
-    rng = np.random.default_rng(vocab)
-    seen_lists = [rng.integers(0, vocab, 64) for _ in range(B)]
     seen = seen_bitmap(seen_lists, vocab)
-    seeds = np.arange(B, dtype=np.int64) * 1000 + 17
-    T, K, P, MP, RP = (np.array([r[i] for r in ROWS]) for i in range(5))
-    step = 5
+    T, K, P, MP, RP = (np.array([r[i] for r in rows]) for i in range(5))
     tokens, logprobs, mask, counts = sample(
         logits, temperature=torch.tensor(T, dtype=torch.float32, device=cuda),
         top_k=torch.tensor(K, dtype=torch.int32, device=cuda), top_p=torch.tensor(P, dtype=torch.float32, device=cuda),
@@ -52,7 +46,7 @@ def test_sampler_matches_oracle(cuda, vocab, dtype):
                                           repetition_penalty=RP[r], seen=seen_row, seed=int(seeds[r]), step=step)
         assert counts[r] == bits[r].sum(), f"row {r}: count"
         if not amb:
-            np.testing.assert_array_equal(bits[r], kept, err_msg=f"row {r} ({ROWS[r]}): kept set")
+            np.testing.assert_array_equal(bits[r], kept, err_msg=f"row {r} ({rows[r]}): kept set")
         if tokens[r] != tok:  # only a float32 near-tie of the race may differ
             xr = x[r].copy()
             if RP[r] != 1.0:
@@ -63,6 +57,35 @@ def test_sampler_matches_oracle(cuda, vocab, dtype):
             assert abs(float(s_gpu) - float(s_ref)) < 1e-4 and bits[r][tokens[r]], f"row {r}: token {tokens[r]} vs {tok}"
         else:
             assert abs(logprobs[r] - lp) < 1e-4, f"row {r}: logprob {logprobs[r]} vs {lp}"
+
+
+@pytest.mark.parametrize("vocab", [151936, 32001, 1000])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sampler_matches_oracle(cuda, vocab, dtype):
+    B = len(ROWS)
+    x = (synth.normal(synth.stream_key("smp", vocab, str(dtype)), B * vocab) * 4.0).astype(np.float32).reshape(B, vocab)
+    rng = np.random.default_rng(vocab)
+    seen_lists = [rng.integers(0, vocab, 64) for _ in range(B)]
+    seeds = np.arange(B, dtype=np.int64) * 1000 + 17
+    _check_rows(cuda, x, ROWS, seen_lists, seeds, 5, dtype)
+
+
+def test_sampler_list_and_full_row_paths(cuda):
+    """Rows that take the one-histogram path (threshold near the max, at most 4,096 candidates) and rows
+    that take the full-row radix passes: a list that would overflow (top_k 5,000; flat logits under
+    top_p), a threshold in the open bin (the 2nd largest 100 below the max)."""
+    V = 151936
+    rows = [(1.0, 3000, 1.0, 0.0, 1.0), (1.0, 5000, 1.0, 0.0, 1.0), (1.0, 2, 1.0, 0.0, 1.0),
+            (1.0, 0, 0.5, 0.0, 1.0), (0.5, 20, 0.7, 0.0, 1.0), (1.0, 0, 0.999, 0.0, 1.0)]
+    x = (synth.normal(synth.stream_key("smp-paths"), len(rows) * V) * 4.0).astype(np.float32).reshape(len(rows), V)
+    x[2] = -200.0
+    x[2, 7] = 0.0
+    x[2, 99] = -100.0
+    x[2, 1234] = -100.0  # a tie at the threshold: both kept
+    x[3] = 0.0  # flat: every token in bin 0
+    seen_lists = [np.zeros(0, np.int64) for _ in rows]
+    seeds = np.arange(len(rows), dtype=np.int64) + 3
+    _check_rows(cuda, x, rows, seen_lists, seeds, 2, torch.float32)
 
 
 def test_sampler_draws_match_kept_softmax(cuda):

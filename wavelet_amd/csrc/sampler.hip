@@ -133,6 +133,91 @@ __device__ __forceinline__ void block_argmax(float &v, int64_t &idx, float *redv
   __syncthreads();
 }
 
+// 64-bit sums and scans over a wave and the 1024-thread block.
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ unsigned long long wave_incl_scan_u64(unsigned long long v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned long long y = __shfl_up(v, o, 64);
+    if (lane >= o) v += y;
+  }
+  return v;
+}
+
+// Exclusive scan of one value per thread in thread order; `total` gets the sum.
+__device__ __forceinline__ unsigned long long block_exscan_u64(unsigned long long v, unsigned long long *red,
+                                                               unsigned long long &total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const unsigned long long incl = wave_incl_scan_u64(v, lane);
+  if (lane == 63) red[w] = incl;
+  __syncthreads();
+  unsigned long long before = 0, all = 0;
+  for (int i = 0; i < kSampleThreads / 64; ++i) {
+    if (i < w) before += red[i];
+    all += red[i];
+  }
+  __syncthreads();
+  total = all;
+  return before + incl - v;
+}
+
+// Radix-select step on a 256-bin histogram, searched from the top bin down:
+// the largest j with above + sum(hist[j..255]) >= target, and the sum
+// strictly above it (bin -1 when no j qualifies). Wave 0 computes it (four
+// bins per lane and one wave scan) and writes it to *bin_out / *cum_out.
+__device__ __forceinline__ void find_from_top(const unsigned long long *hist, unsigned long long above,
+                                              unsigned long long target, uint32_t *bin_out,
+                                              unsigned long long *cum_out) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  unsigned long long h[4], s = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    h[q] = hist[255 - 4 * lane - q];
+    s += h[q];
+  }
+  unsigned long long c = above + wave_incl_scan_u64(s, lane) - s;  // mass of the bins above this lane's
+  int bin = -1;
+  unsigned long long cum = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (bin < 0 && c + h[q] >= target) {
+      bin = 255 - 4 * lane - q;
+      cum = c;
+    }
+    c += h[q];
+  }
+  const unsigned long long hit = __ballot(bin >= 0);
+  if (hit == 0ull) {
+    if (lane == 0) *bin_out = 0xffffffffu;
+  } else if (lane == __ffsll(static_cast<long long>(hit)) - 1) {
+    *bin_out = static_cast<uint32_t>(bin);
+    *cum_out = cum;
+  }
+}
+
+// Fast top_k / top_p: one pass histograms the kept tokens by distance below
+// the row maximum (kBins bins of 1/kBinScale, the last one open-ended), the
+// threshold's bin follows from a block scan, a second pass copies every kept
+// token at or above that bin -- at most kCand of them -- into LDS, and the
+// exact radix selects run over that list. Binning is monotone in the value,
+// so the list holds every token the threshold can keep and the selects give
+// the same keys as over the whole row; rows where the threshold falls in the
+// open bin or the list would overflow take the full-row radix passes.
+constexpr int kBins = 2048;
+constexpr float kBinScale = 32.f;
+constexpr int kCand = 4096;
+static_assert(kBins == 2 * kSampleThreads, "the threshold scan gives every thread two bins");
+
+__device__ __forceinline__ unsigned long long fixed_mass(float x, float mx) {
+  return static_cast<unsigned long long>(expf(x - mx) * 4294967296.f);
+}
+
 struct SampleArgs {
   const float *temperature;  // [B] or NULL (1.0)
   const int32_t *top_k;      // [B] or NULL; <= 0 or >= vocab: off
@@ -156,6 +241,13 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   __shared__ unsigned long long hist[256];
   __shared__ uint32_t sel_prefix;
   __shared__ unsigned long long sel_above;
+  __shared__ unsigned long long red64[kSampleThreads / 64];
+  __shared__ uint32_t fcnt[kBins];
+  __shared__ unsigned long long fmass[kBins];
+  __shared__ uint32_t ckey[kCand];
+  __shared__ float cx[kCand];
+  __shared__ int ncand, sel_bin;
+  __shared__ unsigned long long sel_n;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const T *row = logits + static_cast<int64_t>(b) * row_stride;
@@ -213,9 +305,170 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     key_lo = k > key_lo ? k : key_lo;
   }
 
-  // top_k: radix select of the k-th largest key among kept tokens.
   const int topk = a.top_k ? a.top_k[b] : 0;
-  if (topk > 0 && topk < vocab) {
+  const float tp = a.top_p ? a.top_p[b] : 1.f;
+  const bool want_k = topk > 0 && topk < vocab;
+  const bool want_p = tp < 1.f;
+  const int lane = tid & 63;
+  bool fallback = false;
+  if (want_k || want_p) {
+    // Histogram pass. Masses only for top_p alone (after top_k, top_p runs on the list).
+    const bool hmass = want_p && !want_k;
+    for (int j = tid; j < kBins; j += kSampleThreads) {
+      fcnt[j] = 0u;
+      fmass[j] = 0ull;
+    }
+    if (tid == 0) ncand = 0;
+    __syncthreads();
+    auto bin_of = [&](float x) {
+      const float d = (mx - x) * kBinScale;  // NaN and -inf land in the open bin (and are not kept)
+      return d < static_cast<float>(kBins - 1) ? static_cast<int>(d) : kBins - 1;
+    };
+    uint32_t tcnt = 0;
+    unsigned long long tmass = 0;  // this thread's share of the open bin
+    for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
+      float v[kVec];
+      x8(v, base);
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        if (order_key(v[j]) < key_lo) continue;
+        const int bn = bin_of(v[j]);
+        const unsigned long long m = hmass ? fixed_mass(v[j], mx) : 0ull;
+        if (bn == kBins - 1) {
+          ++tcnt;
+          tmass += m;
+        } else {
+          atomicAdd(&fcnt[bn], 1u);
+          if (hmass) atomicAdd(&fmass[bn], m);
+        }
+      }
+    }
+    const unsigned long long wc = wave_sum_u64(tcnt), wm = wave_sum_u64(tmass);
+    if (lane == 0) {
+      atomicAdd(&fcnt[kBins - 1], static_cast<uint32_t>(wc));
+      if (hmass) atomicAdd(&fmass[kBins - 1], wm);
+    }
+    __syncthreads();
+    // Threshold bin from scans over the bins in value order (bin 0 = nearest the max).
+    const unsigned long long c0 = fcnt[2 * tid], c1 = fcnt[2 * tid + 1];
+    unsigned long long ctot;
+    const unsigned long long cex = block_exscan_u64(c0 + c1, red64, ctot);
+    unsigned long long m0 = 0, m1 = 0, mex = 0, mtot = 0;
+    if (hmass) {
+      m0 = fmass[2 * tid];
+      m1 = fmass[2 * tid + 1];
+      mex = block_exscan_u64(m0 + m1, red64, mtot);
+    }
+    if (tid == 0) sel_bin = -1;
+    __syncthreads();
+    if (want_k) {
+      const unsigned long long kk = static_cast<unsigned long long>(topk);
+      if (ctot >= kk) {  // else fewer than k kept tokens: the full-row path keeps them all
+        if (cex < kk && kk <= cex + c0) {
+          sel_bin = 2 * tid;
+          sel_n = cex + c0;
+        } else if (cex + c0 < kk && kk <= cex + c0 + c1) {
+          sel_bin = 2 * tid + 1;
+          sel_n = cex + c0 + c1;
+        }
+      }
+    } else {
+      const unsigned long long target =
+          static_cast<unsigned long long>(ceil(static_cast<double>(tp) * static_cast<double>(mtot)));
+      if (mex < target && target <= mex + m0) {
+        sel_bin = 2 * tid;
+        sel_n = cex + c0;
+      } else if (mex + m0 < target && target <= mex + m0 + m1) {
+        sel_bin = 2 * tid + 1;
+        sel_n = cex + c0 + c1;
+      }
+    }
+    __syncthreads();
+    const int tb = sel_bin;
+    const unsigned long long n_list = sel_n;
+    fallback = tb < 0 || tb == kBins - 1 || n_list > static_cast<unsigned long long>(kCand);
+    if (!fallback) {
+      // Compaction pass: every kept token at or above the threshold's bin.
+      for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
+        float v[kVec];
+        x8(v, base);
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+          const uint32_t k = order_key(v[j]);
+          const bool take = k >= key_lo && bin_of(v[j]) <= tb;
+          const unsigned long long bal = __ballot(take);
+          if (bal == 0ull) continue;  // uniform: most slots of most passes
+          const int first = __ffsll(static_cast<long long>(bal)) - 1;
+          int at = 0;
+          if (lane == first) at = atomicAdd(&ncand, __popcll(bal));
+          at = __shfl(at, first, 64) + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
+          if (take && at < kCand) {
+            ckey[at] = k;
+            cx[at] = v[j];
+          }
+        }
+      }
+      __syncthreads();
+      const int n = ncand < kCand ? ncand : kCand;  // == n_list
+      // top_k on the list: the k-th largest key (ties kept).
+      if (want_k) {
+        uint32_t prefix = 0, pmask = 0;
+        unsigned long long remaining = static_cast<unsigned long long>(topk);
+        for (int shift = 24; shift >= 0; shift -= 8) {
+          for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
+          __syncthreads();
+          for (int i = tid; i < n; i += kSampleThreads) {
+            const uint32_t k = ckey[i];
+            if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1ull);
+          }
+          __syncthreads();
+          find_from_top(hist, 0ull, remaining, &sel_prefix, &sel_above);  // found: the list holds >= k keys
+          __syncthreads();
+          remaining -= sel_above;
+          prefix |= sel_prefix << shift;
+          pmask |= 255u << shift;
+          __syncthreads();
+        }
+        if (prefix > key_lo) key_lo = prefix;
+      }
+      // top_p on the list. After top_k the list holds every kept token (its
+      // keys >= key_lo), so the kept mass sums over it; top_p alone keeps the
+      // whole row's mass from the histogram pass.
+      if (want_p) {
+        unsigned long long total = mtot;
+        if (want_k) {
+          unsigned long long part = 0;
+          for (int i = tid; i < n; i += kSampleThreads)
+            if (ckey[i] >= key_lo) part += fixed_mass(cx[i], mx);
+          (void)block_exscan_u64(part, red64, total);
+        }
+        const unsigned long long target =
+            static_cast<unsigned long long>(ceil(static_cast<double>(tp) * static_cast<double>(total)));
+        uint32_t prefix = 0, pmask = 0;
+        unsigned long long above = 0;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+          for (int j = tid; j < 256; j += kSampleThreads) hist[j] = 0ull;
+          __syncthreads();
+          for (int i = tid; i < n; i += kSampleThreads) {
+            const uint32_t k = ckey[i];
+            if (k >= key_lo && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], fixed_mass(cx[i], mx));
+          }
+          __syncthreads();
+          find_from_top(hist, above, target, &sel_prefix, &sel_above);
+          __syncthreads();
+          prefix |= sel_prefix << shift;
+          above = sel_above;
+          pmask |= 255u << shift;
+          __syncthreads();
+        }
+        if (prefix > key_lo) key_lo = prefix;
+      }
+    }
+  }
+
+  // top_k over the whole row: radix select of the k-th largest kept key.
+  if (fallback && want_k) {
     uint32_t prefix = 0, pmask = 0;
     unsigned long long remaining = static_cast<unsigned long long>(topk);
     bool enough = true;
@@ -232,19 +485,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
         }
       }
       __syncthreads();
-      if (tid == 0) {
-        unsigned long long cum = 0;
-        int bin = -1;
-        for (int j = 255; j >= 0; --j) {
-          if (cum + hist[j] >= remaining) {
-            bin = j;
-            break;
-          }
-          cum += hist[j];
-        }
-        sel_prefix = static_cast<uint32_t>(bin);  // -1: fewer than k kept tokens
-        sel_above = cum;
-      }
+      find_from_top(hist, 0ull, remaining, &sel_prefix, &sel_above);  // -1: fewer than k kept tokens
       __syncthreads();
       const int bin = static_cast<int>(sel_prefix);
       const unsigned long long above = sel_above;
@@ -260,9 +501,9 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     if (enough && prefix > key_lo) key_lo = prefix;
   }
 
-  // top_p: radix select over fixed-point mass w_i = exp(x_i - max) * 2^32.
-  const float tp = a.top_p ? a.top_p[b] : 1.f;
-  if (tp < 1.f) {
+  // top_p over the whole row: radix select over fixed-point mass
+  // w_i = exp(x_i - max) * 2^32.
+  if (fallback && want_p) {
     unsigned long long total = 0;
     {
       // total kept mass (integer: exact, order-independent)
@@ -299,19 +540,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
         }
       }
       __syncthreads();
-      if (tid == 0) {
-        unsigned long long cum = above;
-        int bin = 0;
-        for (int j = 255; j >= 0; --j) {
-          if (cum + hist[j] >= target) {
-            bin = j;
-            break;
-          }
-          cum += hist[j];
-        }
-        sel_prefix = static_cast<uint32_t>(bin);
-        sel_above = cum;
-      }
+      find_from_top(hist, above, target, &sel_prefix, &sel_above);  // target <= total: always found
       __syncthreads();
       prefix |= sel_prefix << shift;
       above = sel_above;
