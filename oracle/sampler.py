@@ -44,7 +44,9 @@ def log_exp_variates(seed: int, step: int, n: int) -> np.ndarray:
     with np.errstate(over="ignore"):
         stream = mix64(np.uint64(seed) + np.uint64(step) * GOLDEN)
         h = mix64(stream + np.arange(n, dtype=np.uint64))
-    u = ((h >> np.uint64(40)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 16777216.0)
+    # 23 hash bits: u in [2^-24, 1 - 2^-24], exact in float32 (with 24 bits the
+    # top value rounds to 1.0, giving E = 0 and an infinite race score)
+    u = ((h >> np.uint64(41)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 8388608.0)
     return np.log(-np.log(u)).astype(np.float32)
 
 

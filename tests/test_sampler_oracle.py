@@ -84,3 +84,16 @@ def test_hash_stream_is_fixed():
     # the published splitmix64 sequence from state 0: mix(gamma), mix(2 gamma)
     h = S.mix64(np.array([0x9E3779B97F4A7C15, 0x3C6EF372FE94F82A], np.uint64))
     assert [int(x) for x in h] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4]
+
+
+def test_uniform_stays_inside_the_open_interval():
+    """u from the extreme hash values stays strictly inside (0, 1) in float32, so
+    every race score is finite (the top 24-bit value would round to u = 1)."""
+    for top in (np.uint64(0), np.uint64(0xFFFFFFFFFFFFFFFF)):
+        u = ((top >> np.uint64(41)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 8388608.0)
+        assert 0.0 < float(u) < 1.0 and np.isfinite(np.log(-np.log(u)))
+    u24 = ((np.uint64(0xFFFFFFFFFFFFFFFF) >> np.uint64(40)).astype(np.float32) + np.float32(0.5)) * np.float32(
+        1.0 / 16777216.0)
+    assert float(u24) == 1.0  # the mapping this replaced
+    v = S.log_exp_variates(seed=123, step=7, n=200_000)
+    assert np.all(np.isfinite(v))

@@ -23,6 +23,9 @@ namespace wkv {
 
 constexpr int kSampleThreads = 1024;
 constexpr float kGreedyEps = 1e-5f;  // temperatures below this sample greedily
+// A score x - ln E ranges over [x - 2.812, x + 16.636] (u in [2^-24, 1 - 2^-24]):
+// tokens more than 19.45 below the maximum never win the race (20 leaves margin).
+constexpr float kRaceReach = 20.f;
 
 // Order-preserving key of a float (larger float -> larger key); NaN maps below
 // every real value so it is never kept.
@@ -39,10 +42,12 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
   return z ^ (z >> 31);
 }
 
-// ln(E) of the Exp(1) variate of token i: u in (0, 1) from 24 hash bits.
+// ln(E) of the Exp(1) variate of token i: u in [2^-24, 1 - 2^-24] from 23
+// hash bits, exact in float32 (24 bits would round the top value to 1.0:
+// E = 0 and an infinite race score for one token in 2^24).
 __device__ __forceinline__ float log_exp_variate(uint64_t stream, int64_t i) {
   const uint64_t h = mix64(stream + static_cast<uint64_t>(i));
-  const float u = (static_cast<float>(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+  const float u = (static_cast<float>(h >> 41) + 0.5f) * (1.0f / 8388608.0f);
   return logf(-logf(u));
 }
 
@@ -567,8 +572,13 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
           bits |= 1u << j;
           z += expf(v[j] - mx);
           ++cnt;
-          const float score = greedy ? v[j] : v[j] - log_exp_variate(stream, base + j);
-          arg_better(best, bi, score, base + j);
+          // ln E lies in [-16.64, 2.82], so a token below mx - kRaceReach scores
+          // under the maximum's least possible score and cannot win: its draw is skipped.
+          if (greedy) {
+            arg_better(best, bi, v[j], base + j);
+          } else if (v[j] >= mx - kRaceReach) {
+            arg_better(best, bi, v[j] - log_exp_variate(stream, base + j), base + j);
+          }
         }
       }
     }
