@@ -381,18 +381,16 @@ def main() -> int:
     # Per-launch timing of one layer's step (fused append + attention for GQA),
     # layer caches rotated so no layer is re-read from cache.
     def per_launch(fn, reps):
-        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                 for _ in range(reps * args.layers)]
-        i = 0
-        for _ in range(reps):
+        # one event pair around each pass of back-to-back launches over all layers:
+        # the mean device time per layer call, without a gap per launch
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in pairs:
+            a.record()
             for layer in range(args.layers):
-                a, b = pairs[i]
-                a.record()
                 fn(layer)
-                b.record()
-                i += 1
+            b.record()
         torch.cuda.synchronize()
-        return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3
+        return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3 / args.layers
 
     kernel_us = per_launch(step.step_layer, args.kernel_reps)
     split = wl.get("split", True)  # the step has separate append and attention calls
@@ -426,6 +424,12 @@ def main() -> int:
         }
         print(json.dumps(rec), flush=True)
         return 0
+    kernel_name = wl["kernel"]
+    if ",W>" in kernel_name:  # the plain decode: the library's waves per workgroup for this geometry
+        from wavelet_amd import decode_plan
+
+        _, waves, _ = decode_plan(w.batch, w.num_kv_heads, int(w.context_lens.max()), w.block_size, args.partition)
+        kernel_name = kernel_name.replace(",W>", f",{waves}>")
     rec = {
         "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx" if headline
         else wl.get("metric", f"decode-attn+KV-append GB/s & us/step, {wl['name']}"),
@@ -451,12 +455,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": wl["kernel"].replace(",W>", ",4>") if headline else wl["kernel"],
+            "kernel": kernel_name,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("decode_gqa_kernel<128,false,true,4>") if headline else None,
+            "traffic": measured_traffic(kernel_name) if headline else None,
             "bytes_per_launch": wl["layer_bytes"],
             "mean_launch_us": round(kernel_us, 2),
             "tflops": round(wl["flops_per_layer"] / (kernel_us * 1e-6) / 1e12, 2),

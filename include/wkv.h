@@ -162,6 +162,15 @@ int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stri
  * batch order); an addition of this library's. */
 int wkv_decode_order(const int32_t *seq_lens, int32_t batch, int32_t *order, void *stream);
 
+/* The launch shape the two GQA decode calls use for this geometry (host
+ * only, no GPU): the partition size (partition_size, or the library's choice
+ * when 0), the waves per workgroup and the workgroups (chunks) per sequence
+ * and KV head; more than one chunk leaves partials for the merge kernel. For
+ * planning and labelling; no reference counterpart. max_seq_len is the one
+ * the decode call will get, clipped to the block-table width. */
+int wkv_decode_plan(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len, int32_t block_size,
+                    int32_t partition_size, int32_t *out_partition, int32_t *out_waves, int32_t *out_chunks);
+
 /* One whole decode step of one layer in one launch: append token b of
  * key/value ([batch, num_kv_heads, head_dim] bf16) at slot_mapping[b] (-1 =
  * none) -- bf16 as wkv_append, fp8 as wkv_append_fp8 with runs of one -- then

@@ -155,3 +155,23 @@ def test_status_codes_map_to_python_exceptions():
         _lib.check(_lib.WKV_ERR_UNSUPPORTED, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.WKV_ERR_LAUNCH, "x")
+
+
+def test_decode_plan_shapes_and_errors():
+    """The launch shape is host logic: an eighth of the longest context per wave (8-wave workgroups),
+    fewer tokens when the batch is too small to fill the GPU, never below 128 tokens or above 64 blocks."""
+    from wavelet_amd import decode_plan
+
+    assert decode_plan(64, 8, 4096, 16) == (512, 8, 1)  # Qwen3-4B headline
+    assert decode_plan(64, 8, 8192, 16) == (1024, 8, 1)  # var-length, longest 8,192
+    assert decode_plan(128, 2, 2048, 16) == (256, 8, 1)  # Qwen2.5-0.5B
+    assert decode_plan(1, 8, 4096, 16) == (128, 8, 4)  # one sequence: more, shorter partitions
+    assert decode_plan(64, 8, 65536, 16) == (1024, 8, 8)  # long context: 1,024-token partitions, merged
+    assert decode_plan(64, 8, 4096, 16, 1024) == (1024, 4, 1)  # the caller's partition wins
+    assert decode_plan(64, 8, 100, 16) == (128, 1, 1)
+    assert decode_plan(64, 8, 4096, 64) == (512, 8, 1)
+    lib = _lib.load()
+    o = ctypes.c_int32()
+    assert lib.wkv_decode_plan(64, 8, 4096, 8, 0, ctypes.byref(o), ctypes.byref(o), ctypes.byref(o)) == _lib.WKV_ERR_INVALID
+    assert lib.wkv_decode_plan(64, 0, 4096, 16, 0, ctypes.byref(o), ctypes.byref(o), ctypes.byref(o)) == _lib.WKV_ERR_INVALID
+    assert lib.wkv_decode_plan(64, 8, 4096, 16, 0, None, ctypes.byref(o), ctypes.byref(o)) == _lib.WKV_ERR_INVALID

@@ -5,7 +5,8 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
 * ``PagedKVCache`` / ``MLALatentCache`` -- per-layer caches with ``append``,
   ``gather`` and ``copy_blocks``;
 * ``paged_decode_gqa`` / ``paged_decode_mla`` -- one decode step of attention;
-  ``decode_order`` -- a step's longest-first dispatch order for the former;
+  ``decode_order`` -- a step's longest-first dispatch order for the former,
+  ``decode_plan`` -- its launch shape;
 * ``paged_decode_gqa_grouped`` -- the same for GRPO groups, reading each
   group's shared prompt blocks once;
 * ``prefill_gqa`` -- varlen (chunked) prefill that appends the prompt's K/V
@@ -18,7 +19,7 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
   top_p, repetition penalty; processed logprobs and the sampling mask).
 """
 
-from .attention import decode_order, paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla, prefill_gqa
+from .attention import decode_order, decode_plan, paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla, prefill_gqa
 from .blocks import BlockManager
 from .cache import MLALatentCache, PagedKVCache, validate_tables
 from .pool import KVPool
@@ -30,6 +31,7 @@ __all__ = [
     "MLALatentCache",
     "PagedKVCache",
     "decode_order",
+    "decode_plan",
     "paged_decode_gqa",
     "paged_decode_gqa_grouped",
     "paged_decode_mla",

@@ -51,6 +51,17 @@ def _max_len(seq_lens: torch.Tensor, max_seq_len: int | None) -> int:
     return int(seq_lens.max().item()) if seq_lens.numel() else 0
 
 
+def decode_plan(batch: int, num_kv_heads: int, max_seq_len: int, block_size: int,
+                partition_size: int = 0) -> tuple[int, int, int]:
+    """(partition size, waves per workgroup, workgroups per sequence and KV head)
+    that ``paged_decode_gqa`` launches for this geometry (host-side, no GPU)."""
+    p, w, c = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    _lib.check(_lib.load().wkv_decode_plan(int(batch), int(num_kv_heads), int(max_seq_len), int(block_size),
+                                           int(partition_size), ctypes.byref(p), ctypes.byref(w), ctypes.byref(c)),
+               "decode_plan")
+    return p.value, w.value, c.value
+
+
 def decode_order(seq_lens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Dispatch order for ``paged_decode_gqa``: int32 ``[B]`` sequence indices by
     ``seq_lens``, longest first, ties by index (computed on the device).

@@ -569,13 +569,19 @@ struct GroupSlots {
 // partition waves over the longest context -- every CU's resident slots in
 // about one round, and no more (fewer, longer waves amortise the per-wave
 // prologue and the partial-result traffic; measured, d=64 contexts of
-// 256..2,048 tokens run 8% faster at 2,048 than at 4,096 waves) -- at least
-// 128 tokens, a multiple of the block size (the fused append relies on it),
-// and at most 64 blocks (one lane each).
+// 256..2,048 tokens run 8% faster at 2,048 than at 4,096 waves) but at most
+// an eighth of the longest context, at least 128 tokens, a multiple of the
+// block size (the fused append relies on it), and at most 64 blocks (one
+// lane each).
 static int choose_partition(int batch, int hkv, int max_seq_len, int BS) {
   const int64_t target_waves = 2048;
   const int64_t items = static_cast<int64_t>(batch) * hkv;
   int64_t p = (items * max_seq_len + target_waves - 1) / target_waves;
+  // An eighth of the longest context: every sequence gets eight waves, one
+  // 8-wave workgroup while that fits (headline shape -1%, fp8 GRPO groups -3%
+  // against the wave target alone).
+  const int64_t eighth = (static_cast<int64_t>(max_seq_len) + 7) / 8;
+  if (p > eighth) p = eighth;
   const int64_t unit = BS;  // a multiple of 16 already
   p = (p + unit - 1) / unit * unit;
   const int64_t lo = (128 + unit - 1) / unit * unit;
@@ -587,9 +593,35 @@ static int choose_partition(int batch, int hkv, int max_seq_len, int BS) {
   return static_cast<int>(p);
 }
 
+// Waves per workgroup and chunks per sequence: partitions of one context
+// share a workgroup (and an LDS merge) up to 8 at a time; longer contexts
+// leave per-chunk partials. (8-wave workgroups for 8+ partitions: var-length
+// Qwen3-4B -7%, Qwen2.5-0.5B -11% against 4.)
+static void decode_shape(int max_seq, int partition_size, int *W, int *chunks) {
+  const int max_parts = max_seq > 0 ? (max_seq + partition_size - 1) / partition_size : 1;
+  *W = max_parts <= 1 ? 1 : (max_parts <= 2 ? 2 : (max_parts < 8 ? 4 : 8));
+  *chunks = (max_parts + *W - 1) / *W;
+}
+
 }  // namespace wkv
 
 using namespace wkv;
+
+extern "C" int wkv_decode_plan(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len, int32_t block_size,
+                               int32_t partition_size, int32_t *out_partition, int32_t *out_waves,
+                               int32_t *out_chunks) {
+  WKV_CHECK_ARG(batch >= 0 && num_kv_heads > 0 && max_seq_len >= 0 && partition_size >= 0,
+                "bad decode geometry");
+  WKV_CHECK_ARG(block_size > 0 && block_size % 16 == 0, "block_size must be a positive multiple of 16");
+  WKV_CHECK_ARG(out_partition && out_waves && out_chunks, "output pointer is NULL");
+  const int p = partition_size != 0 ? partition_size : choose_partition(batch, num_kv_heads, max_seq_len, block_size);
+  int W, chunks;
+  decode_shape(max_seq_len, p, &W, &chunks);
+  *out_partition = p;
+  *out_waves = W;
+  *out_chunks = chunks;
+  return WKV_OK;
+}
 
 extern "C" int64_t wkv_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim,
                                              int32_t max_seq_len, int32_t partition_size) {
@@ -658,14 +690,9 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   if (ap != nullptr)
     WKV_CHECK_ARG(partition_size % BS == 0, "a fused append needs partition_size %d to be a multiple of block_size %d",
                   partition_size, BS);
-  const int max_parts = max_seq > 0 ? (max_seq + partition_size - 1) / partition_size : 1;
-  // Waves per workgroup: partitions of one context share a workgroup (and an
-  // LDS merge) up to 8 at a time; longer contexts leave per-chunk partials.
-  // (8-wave workgroups for 8+ partitions: var-length Qwen3-4B -7%, Qwen2.5-0.5B
-  // -11% against 4; the 4-partition headline shape stays at 4.)
-  const int W = max_parts <= 1 ? 1 : (max_parts <= 2 ? 2 : (max_parts < 8 ? 4 : 8));
-  const int max_chunks = (max_parts + W - 1) / W;
-  WKV_CHECK_ARG(max_chunks <= 65535, "too many partitions (%d)", max_parts);
+  int W, max_chunks;
+  decode_shape(max_seq, partition_size, &W, &max_chunks);
+  WKV_CHECK_ARG(max_chunks <= 65535, "too many partitions");
   const int64_t need = wkv_decode_workspace_size(batch, num_q_heads, D, max_seq, partition_size * W);
   if (max_chunks > 1)
     WKV_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= need,
