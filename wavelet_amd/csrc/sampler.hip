@@ -16,6 +16,7 @@
 // Outputs: the token, its processed logprob (log-softmax over the kept set of
 // the processed logits), the kept set as a bitmap and its size.
 #include <cmath>
+#include <type_traits>
 
 #include "wkv_common.h"
 
@@ -120,12 +121,16 @@ __device__ __forceinline__ void arg_better(float &v, int64_t &i, float ov, int64
 }
 
 __device__ __forceinline__ void block_argmax(float &v, int64_t &idx, float *redv, int64_t *redi) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int64_t oi = __shfl_xor(idx, o, 64);
-    arg_better(v, idx, ov, oi);
-  }
+  const auto step = [&](auto o) {
+    constexpr int O = decltype(o)::value;
+    arg_better(v, idx, lane_xor<O>(v), lane_xor<O>(idx));
+  };
+  step(std::integral_constant<int, 32>{});
+  step(std::integral_constant<int, 16>{});
+  step(std::integral_constant<int, 8>{});
+  step(std::integral_constant<int, 4>{});
+  step(std::integral_constant<int, 2>{});
+  step(std::integral_constant<int, 1>{});
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     redv[w] = v;
@@ -140,9 +145,7 @@ __device__ __forceinline__ void block_argmax(float &v, int64_t &idx, float *redv
 
 // 64-bit sums and scans over a wave and the 1024-thread block.
 __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  return wave_reduce(v, [](unsigned long long a, unsigned long long b) { return a + b; });
 }
 
 __device__ __forceinline__ unsigned long long wave_incl_scan_u64(unsigned long long v, int lane) {

@@ -140,16 +140,73 @@ constexpr float SOFTMAX_TAU = 8.f;
 
 // ---------------------------------------------------------------------------
 // Wavefront helpers (wave64).
+
+// The value lane (lane ^ O) holds, for O a power of two below 64, with no
+// address register (a ds_bpermute needs one per distance, which the compiler
+// keeps live across a kernel): the cross-row swaps of gfx950 for 32 and 16
+// (each returns {vdst, src} after the swap: the lane's own row in one, the
+// partner row in the other), a DPP row rotate by 8 (within 16 lanes that is
+// the xor), the LDS swizzle's bitmask mode for 4 and DPP quad permutes for 2
+// and 1.
+template <int O>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
+  static_assert(O >= 1 && O <= 32 && (O & (O - 1)) == 0, "lane_xor: a power of two below 64");
+  if constexpr (O == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (__lane_id() & 32) ? r[0] : r[1];
+  } else if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (__lane_id() & 16) ? r[0] : r[1];
+  } else if constexpr (O == 8) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x128, 0xF, 0xF, false));
+  } else if constexpr (O == 4) {
+    return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(x), (4 << 10) | 0x1F));
+  } else if constexpr (O == 2) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x4E, 0xF, 0xF, false));
+  } else {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0xB1, 0xF, 0xF, false));
+  }
+}
+
+template <int O>
+__device__ __forceinline__ float lane_xor(float x) {
+  return __uint_as_float(lane_xor<O>(__float_as_uint(x)));
+}
+
+template <int O>
+__device__ __forceinline__ int lane_xor(int x) {
+  return static_cast<int>(lane_xor<O>(static_cast<uint32_t>(x)));
+}
+
+template <int O>
+__device__ __forceinline__ unsigned long long lane_xor(unsigned long long x) {
+  const uint32_t lo = lane_xor<O>(static_cast<uint32_t>(x)), hi = lane_xor<O>(static_cast<uint32_t>(x >> 32));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+template <int O>
+__device__ __forceinline__ int64_t lane_xor(int64_t x) {
+  return static_cast<int64_t>(lane_xor<O>(static_cast<unsigned long long>(x)));
+}
+
+// f folded over the xor butterfly 32, 16, ..., 1: every lane ends with the
+// same result, combined in the same order as a __shfl_xor loop.
+template <class T, class F>
+__device__ __forceinline__ T wave_reduce(T v, F f) {
+  v = f(v, lane_xor<32>(v));
+  v = f(v, lane_xor<16>(v));
+  v = f(v, lane_xor<8>(v));
+  v = f(v, lane_xor<4>(v));
+  v = f(v, lane_xor<2>(v));
+  return f(v, lane_xor<1>(v));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
 }  // namespace wkv
