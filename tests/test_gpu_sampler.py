@@ -88,6 +88,33 @@ def test_sampler_list_and_full_row_paths(cuda):
     _check_rows(cuda, x, rows, seen_lists, seeds, 2, torch.float32)
 
 
+def test_sampler_capture_paths(cuda):
+    """Rows for the one-capture-pass list: top_k whose range holds fewer kept tokens than k (min_p),
+    k equal to the thread count, a flat row whose range overflows the list (histogram, then full-row
+    passes), top_p alone and top_k + top_p on peaked logits (the list holds the threshold), greedy
+    with top_k (the list's argmax)."""
+    V = 151936
+    rows = [(1.0, 50, 1.0, 0.5, 1.0), (1.0, 1024, 1.0, 0.0, 1.0), (1.0, 20, 1.0, 0.0, 1.0),
+            (1.0, 0, 0.9, 0.0, 1.0), (0.7, 50, 0.9, 0.0, 1.0), (0.0, 50, 1.0, 0.0, 1.0), (1.0, 0, 0.995, 0.0, 1.2)]
+    x = (synth.normal(synth.stream_key("smp-capture"), len(rows) * V) * 4.0).astype(np.float32).reshape(len(rows), V)
+    x[2] = 0.0
+    x[3:] *= 10.0
+    rng = np.random.default_rng(7)
+    seen_lists = [rng.integers(0, V, 200) for _ in rows]
+    seeds = np.arange(len(rows), dtype=np.int64) + 11
+    _check_rows(cuda, x, rows, seen_lists, seeds, 4, torch.float32)
+
+
+def test_sampler_vocab_beyond_lds_mask(cuda):
+    """300,000 tokens (9,375 mask words): the list path keeps the full-row final pass."""
+    V = 300000
+    rows = [(0.7, 50, 0.9, 0.0, 1.0), (1.0, 0, 0.9, 0.0, 1.0), (1.0, 0, 1.0, 0.0, 1.0)]
+    x = (synth.normal(synth.stream_key("smp-300k"), len(rows) * V) * 40.0).astype(np.float32).reshape(len(rows), V)
+    seen_lists = [np.zeros(0, np.int64) for _ in rows]
+    seeds = np.arange(len(rows), dtype=np.int64) + 5
+    _check_rows(cuda, x, rows, seen_lists, seeds, 1, torch.bfloat16)
+
+
 def test_sampler_draws_match_kept_softmax(cuda):
     """8,192 independent rows (seeds 0..8191) of the same 8 logits in one launch."""
     x = np.array([2.0, 1.0, 0.5, 0.0, -1.0, 3.0, -5.0, 1.5], np.float32)

@@ -45,9 +45,15 @@ HIPCC_FLAGS = [
 #   per tile, measured in the ISA), whether or not a rescale happens. Its
 #   kernels need at most ~200 registers, so nothing is lost. (decode_mla.hip
 #   keeps AGPRs: its 1-wave-per-SIMD kernels use more than 256 registers.)
+#   sampler.hip: no machine sinking. Its passes issue the loads of several
+#   row chunks before using the first; the sinking pass moves each load back
+#   down to its first use (into the branches that follow), leaving one load
+#   in flight per thread (measured in the ISA: 4 batched loads in the max
+#   pass only; the sampler 4% slower).
 EXTRA_FLAGS = {
     "decode_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "prefill_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],  # the same tile code
+    "sampler.hip": ["-mllvm", "-disable-machine-sink"],
 }
 
 

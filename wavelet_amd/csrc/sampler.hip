@@ -64,25 +64,53 @@ __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *row, int64
 // Elements per thread per step: 8 consecutive logits, one or two 16-byte loads
 // when the row allows it (`vec`), element loads otherwise; -inf past the end.
 constexpr int kVec = 8;
+// Chunks a pass keeps in flight per thread: the loads of kBatch chunks issue
+// before the first is used (with one 16-byte load per thread at a time a pass
+// over a row is bound by the load latency, not by HBM).
+constexpr int kBatch = 4;
+
+// One chunk's raw bits: 16 bytes of bf16, or 32 of fp32.
+template <typename T>
+struct Chunk;
+template <>
+struct Chunk<uint16_t> {
+  u32x4 w;
+};
+template <>
+struct Chunk<float> {
+  floatx4 a, b;
+};
+
+template <typename T>
+__device__ __forceinline__ Chunk<T> load_chunk(const T *p) {
+  if constexpr (sizeof(T) == 2) {
+    return Chunk<T>{*reinterpret_cast<const u32x4 *>(p)};
+  } else {
+    return Chunk<T>{*reinterpret_cast<const floatx4 *>(p), *reinterpret_cast<const floatx4 *>(p + 4)};
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack_chunk(const Chunk<T> &c, float v[kVec]) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = __uint_as_float(c.w[j] << 16);
+      v[2 * j + 1] = __uint_as_float(c.w[j] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = c.a[j];
+      v[4 + j] = c.b[j];
+    }
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ void load8(float v[kVec], const T *row, int64_t base, int vocab, bool vec) {
   if (vec && base + kVec <= vocab) {
-    if constexpr (sizeof(T) == 2) {
-      const u32x4 w = *reinterpret_cast<const u32x4 *>(row + base);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = __uint_as_float(w[j] << 16);
-        v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-      }
-    } else {
-      const floatx4 a = *reinterpret_cast<const floatx4 *>(row + base);
-      const floatx4 b = *reinterpret_cast<const floatx4 *>(row + base + 4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[j] = a[j];
-        v[4 + j] = b[j];
-      }
-    }
+    unpack_chunk<T>(load_chunk<T>(row + base), v);
   } else {
 #pragma unroll
     for (int j = 0; j < kVec; ++j) v[j] = base + j < vocab ? load_logit<T>(row, base + j) : -INFINITY;
@@ -209,17 +237,27 @@ __device__ __forceinline__ void find_from_top(const unsigned long long *hist, un
   }
 }
 
-// Fast top_k / top_p: one pass histograms the kept tokens by distance below
-// the row maximum (kBins bins of 1/kBinScale, the last one open-ended), the
-// threshold's bin follows from a block scan, a second pass copies every kept
-// token at or above that bin -- at most kCand of them -- into LDS, and the
-// exact radix selects run over that list. Binning is monotone in the value,
-// so the list holds every token the threshold can keep and the selects give
-// the same keys as over the whole row; rows where the threshold falls in the
-// open bin or the list would overflow take the full-row radix passes.
+// Fast top_k / top_p. Every kept token the threshold can keep lies within a
+// range below the row maximum known before the second pass (top_k: the bin of
+// the k-th largest of the threads' maxima; top_p alone: a bound on the tail's
+// weight), so one capture pass copies the kept tokens in that range -- at
+// most kCand of them -- into an LDS list, the exact radix selects run over
+// the list and the draw, mass and mask come from it too. Rows whose range
+// holds more tokens take a histogram of the kept tokens by distance below the
+// maximum (kBins bins of 1/kBinScale, the last one open-ended), whose block
+// scan gives the threshold's bin, and a compaction pass of the kept tokens at
+// or above it. Binning is monotone in the value, so the list holds every
+// token the threshold can keep and the selects give the same keys as over the
+// whole row; rows whose threshold still falls in the open bin or overflows
+// the list take the full-row radix passes.
 constexpr int kBins = 2048;
 constexpr float kBinScale = 32.f;
 constexpr int kCand = 4096;
+// A token this many bins or more below the maximum (22.2 nats) weighs under
+// one unit of fixed_mass: exactly 0.
+constexpr int kMassBins = 711;
+// Rows of up to kMaskWords * 32 tokens build their mask in LDS on the list path.
+constexpr int kMaskWords = 8192;
 static_assert(kBins == 2 * kSampleThreads, "the threshold scan gives every thread two bins");
 
 __device__ __forceinline__ unsigned long long fixed_mass(float x, float mx) {
@@ -254,6 +292,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   __shared__ unsigned long long fmass[kBins];
   __shared__ uint32_t ckey[kCand];
   __shared__ float cx[kCand];
+  __shared__ int32_t cidx[kCand];
+  __shared__ uint32_t mbits[kMaskWords];
   __shared__ int ncand, sel_bin;
   __shared__ unsigned long long sel_n;
   const int b = blockIdx.x;
@@ -272,8 +312,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     return l * inv_t;
   };
   // The 8 processed logits at base .. base+7 (-inf past the end).
-  auto x8 = [&](float v[kVec], int64_t base) {
-    load8<T>(v, row, base, vocab, vec);
+  auto processed = [&](float v[kVec], int64_t base) {
     if (seen) {
       const uint32_t w = seen[base >> 5] >> (base & 31);  // base is a multiple of 8: one word
 #pragma unroll
@@ -283,18 +322,55 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
 #pragma unroll
     for (int j = 0; j < kVec; ++j) v[j] *= inv_t;
   };
+  auto x8 = [&](float v[kVec], int64_t base) {
+    load8<T>(v, row, base, vocab, vec);
+    processed(v, base);
+  };
   const int64_t step8 = static_cast<int64_t>(kSampleThreads) * kVec;
-
-  // Pass 1: max (and the greedy argmax).
-  float mx = -INFINITY;
-  int64_t amx = 0x7fffffffffffffffll;
-  for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
-    float v[kVec];
-    x8(v, base);
+  // f(v, base) over this thread's chunks in row order, kBatch loads in flight.
+  // With EVERY the trip count is uniform and f also sees the chunks past the
+  // end (all -inf), so every lane of a wave makes the same calls.
+  auto for_chunks = [&](auto every, auto &&f) {
+    constexpr bool EVERY = decltype(every)::value;
+    for (int64_t c0 = 0; c0 < vocab; c0 += kBatch * step8) {
+      const int64_t t0 = c0 + static_cast<int64_t>(tid) * kVec;
+      if (vec && c0 + kBatch * step8 <= vocab) {  // uniform: every chunk of the batch is whole
+        Chunk<T> r[kBatch];
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) arg_better(mx, amx, v[j], base + j);
-  }
-  block_argmax(mx, amx, redv, redi);
+        for (int u = 0; u < kBatch; ++u) r[u] = load_chunk<T>(row + t0 + u * step8);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          float v[kVec];
+          unpack_chunk<T>(r[u], v);
+          processed(v, t0 + u * step8);
+          f(v, t0 + u * step8);
+        }
+      } else {
+        for (int u = 0; u < kBatch; ++u) {
+          const int64_t base = t0 + u * step8;
+          float v[kVec];
+          if (base < vocab) {
+            x8(v, base);
+          } else {
+            if (!EVERY) break;
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) v[j] = -INFINITY;
+          }
+          f(v, base);
+        }
+      }
+    }
+  };
+  using Every = std::true_type;
+  using Own = std::false_type;
+
+  // Pass 1: the row maximum; each thread keeps its own (top_k's capture range).
+  float tmx = -INFINITY;
+  for_chunks(Own{}, [&](const float v[kVec], int64_t) {
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) tmx = fmaxf(tmx, v[j]);  // NaN never wins
+  });
+  const float mx = block_max(tmx, redv);
   if (!(mx > -INFINITY)) {  // nothing finite: token 0, empty support
     if (tid == 0) {
       a.tokens[b] = 0;
@@ -319,108 +395,183 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   const bool want_p = tp < 1.f;
   const int lane = tid & 63;
   bool fallback = false;
+  bool listed = false;  // the LDS list holds every kept token the threshold can keep
+  int n = 0;            // its length
+  unsigned long long mtot = 0;  // the kept mass of the row (top_p alone)
+  auto bin_of = [&](float x) {
+    const float d = (mx - x) * kBinScale;  // NaN and -inf land in the open bin (and are not kept)
+    return d < static_cast<float>(kBins - 1) ? static_cast<int>(d) : kBins - 1;
+  };
+  // Appends the kept tokens with `take` set to the list (one LDS atomic per
+  // wave and slot); every lane of the wave that is still in the pass calls it.
+  auto append = [&](bool take, uint32_t k, float x, int64_t t) {
+    const unsigned long long bal = __ballot(take);
+    if (bal == 0ull) return;  // uniform: most slots of most passes
+    const int first = __ffsll(static_cast<long long>(bal)) - 1;
+    int at = 0;
+    if (lane == first) at = atomicAdd(&ncand, __popcll(bal));
+    at = __shfl(at, first, 64) + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
+    if (take && at < kCand) {
+      ckey[at] = k;
+      cx[at] = x;
+      cidx[at] = static_cast<int32_t>(t);
+    }
+  };
   if (want_k || want_p) {
-    // Histogram pass. Masses only for top_p alone (after top_k, top_p runs on the list).
-    const bool hmass = want_p && !want_k;
+    const bool hmass = want_p && !want_k;  // after top_k, top_p runs on the list
     for (int j = tid; j < kBins; j += kSampleThreads) {
       fcnt[j] = 0u;
       fmass[j] = 0ull;
     }
-    if (tid == 0) ncand = 0;
+    if (tid == 0) {
+      ncand = 0;
+      sel_n = 0ull;
+    }
     __syncthreads();
-    auto bin_of = [&](float x) {
-      const float d = (mx - x) * kBinScale;  // NaN and -inf land in the open bin (and are not kept)
-      return d < static_cast<float>(kBins - 1) ? static_cast<int>(d) : kBins - 1;
-    };
-    uint32_t tcnt = 0;
-    unsigned long long tmass = 0;  // this thread's share of the open bin
-    for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
-      float v[kVec];
-      x8(v, base);
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        if (order_key(v[j]) < key_lo) continue;
-        const int bn = bin_of(v[j]);
-        const unsigned long long m = hmass ? fixed_mass(v[j], mx) : 0ull;
-        if (bn == kBins - 1) {
-          ++tcnt;
-          tmass += m;
-        } else {
-          atomicAdd(&fcnt[bn], 1u);
-          if (hmass) atomicAdd(&fmass[bn], m);
-        }
+
+    // Capture range, in bins below the maximum, holding every token the
+    // threshold can keep. top_k (k <= threads): the k largest of the threads'
+    // maxima are k distinct tokens, so the row's k-th largest lies in or above
+    // the bin of their k-th. top_p alone: tokens more than
+    // r = ln(vocab / (1 - top_p)) + 1 below the maximum weigh at most
+    // (1 - top_p) / e of the maximum's weight all together, so the mass above
+    // the threshold is reached within r (the maximum's fixed-point weight is
+    // exactly 2^32, whence the kept mass is at least that).
+    int bcap = kBins - 1;
+    if (want_k && topk <= kSampleThreads) {
+      atomicAdd(&fcnt[bin_of(tmx)], 1u);
+      __syncthreads();
+      const unsigned long long c0 = fcnt[2 * tid], c1 = fcnt[2 * tid + 1];
+      unsigned long long ctot;
+      const unsigned long long cex = block_exscan_u64(c0 + c1, red64, ctot);
+      const unsigned long long kk = static_cast<unsigned long long>(topk);
+      if (tid == 0) sel_bin = kBins - 1;
+      __syncthreads();
+      if (cex < kk && kk <= cex + c0)
+        sel_bin = 2 * tid;
+      else if (cex + c0 < kk && kk <= cex + c0 + c1)
+        sel_bin = 2 * tid + 1;
+      fcnt[2 * tid] = 0u;
+      fcnt[2 * tid + 1] = 0u;
+      __syncthreads();
+      bcap = sel_bin;
+    } else if (!want_k) {
+      const double tail = 1.0 - static_cast<double>(tp);
+      if (tail > 1e-6) {
+        const double r = (log(static_cast<double>(vocab) / tail) + 1.0) * static_cast<double>(kBinScale);
+        bcap = r < static_cast<double>(kBins - 1) ? static_cast<int>(ceil(r)) : kBins - 1;
       }
     }
-    const unsigned long long wc = wave_sum_u64(tcnt), wm = wave_sum_u64(tmass);
-    if (lane == 0) {
-      atomicAdd(&fcnt[kBins - 1], static_cast<uint32_t>(wc));
-      if (hmass) atomicAdd(&fmass[kBins - 1], wm);
+
+    // Capture pass: the kept tokens within the range go to the list; the
+    // kept mass sums over the whole row (a token kMassBins or more below the
+    // maximum weighs under one fixed-point unit: exactly 0).
+    if (bcap < kBins - 1) {
+      unsigned long long tmass = 0;
+      for_chunks(Own{}, [&](const float v[kVec], int64_t base) {
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+          const uint32_t k = order_key(v[j]);
+          const int bn = bin_of(v[j]);
+          if (hmass && k >= key_lo && bn < kMassBins) tmass += fixed_mass(v[j], mx);
+          append(k >= key_lo && bn <= bcap, k, v[j], base + j);
+        }
+      });
+      if (hmass) {
+        const unsigned long long wm = wave_sum_u64(tmass);
+        if (lane == 0) atomicAdd(&sel_n, wm);
+      }
+      __syncthreads();
+      n = ncand;
+      listed = n <= kCand;
+      mtot = sel_n;
+      __syncthreads();
     }
-    __syncthreads();
-    // Threshold bin from scans over the bins in value order (bin 0 = nearest the max).
-    const unsigned long long c0 = fcnt[2 * tid], c1 = fcnt[2 * tid + 1];
-    unsigned long long ctot;
-    const unsigned long long cex = block_exscan_u64(c0 + c1, red64, ctot);
-    unsigned long long m0 = 0, m1 = 0, mex = 0, mtot = 0;
-    if (hmass) {
-      m0 = fmass[2 * tid];
-      m1 = fmass[2 * tid + 1];
-      mex = block_exscan_u64(m0 + m1, red64, mtot);
-    }
-    if (tid == 0) sel_bin = -1;
-    __syncthreads();
-    if (want_k) {
-      const unsigned long long kk = static_cast<unsigned long long>(topk);
-      if (ctot >= kk) {  // else fewer than k kept tokens: the full-row path keeps them all
-        if (cex < kk && kk <= cex + c0) {
+
+    if (!listed) {
+      // Histogram pass over the whole row, then a compaction pass: every kept
+      // token at or above the threshold's bin.
+      if (tid == 0) ncand = 0;
+      uint32_t tcnt = 0;
+      unsigned long long tmass = 0;  // this thread's share of the open bin
+      for_chunks(Own{}, [&](const float v[kVec], int64_t) {
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+          if (order_key(v[j]) < key_lo) continue;
+          const int bn = bin_of(v[j]);
+          const unsigned long long m = hmass ? fixed_mass(v[j], mx) : 0ull;
+          if (bn == kBins - 1) {
+            ++tcnt;
+            tmass += m;
+          } else {
+            atomicAdd(&fcnt[bn], 1u);
+            if (hmass) atomicAdd(&fmass[bn], m);
+          }
+        }
+      });
+      const unsigned long long wc = wave_sum_u64(tcnt), wm = wave_sum_u64(tmass);
+      if (lane == 0) {
+        atomicAdd(&fcnt[kBins - 1], static_cast<uint32_t>(wc));
+        if (hmass) atomicAdd(&fmass[kBins - 1], wm);
+      }
+      __syncthreads();
+      // Threshold bin from scans over the bins in value order (bin 0 = nearest the max).
+      const unsigned long long c0 = fcnt[2 * tid], c1 = fcnt[2 * tid + 1];
+      unsigned long long ctot;
+      const unsigned long long cex = block_exscan_u64(c0 + c1, red64, ctot);
+      unsigned long long m0 = 0, m1 = 0, mex = 0;
+      if (hmass) {
+        m0 = fmass[2 * tid];
+        m1 = fmass[2 * tid + 1];
+        mex = block_exscan_u64(m0 + m1, red64, mtot);
+      }
+      if (tid == 0) sel_bin = -1;
+      __syncthreads();
+      if (want_k) {
+        const unsigned long long kk = static_cast<unsigned long long>(topk);
+        if (ctot >= kk) {  // else fewer than k kept tokens: the full-row path keeps them all
+          if (cex < kk && kk <= cex + c0) {
+            sel_bin = 2 * tid;
+            sel_n = cex + c0;
+          } else if (cex + c0 < kk && kk <= cex + c0 + c1) {
+            sel_bin = 2 * tid + 1;
+            sel_n = cex + c0 + c1;
+          }
+        }
+      } else {
+        const unsigned long long target =
+            static_cast<unsigned long long>(ceil(static_cast<double>(tp) * static_cast<double>(mtot)));
+        if (mex < target && target <= mex + m0) {
           sel_bin = 2 * tid;
           sel_n = cex + c0;
-        } else if (cex + c0 < kk && kk <= cex + c0 + c1) {
+        } else if (mex + m0 < target && target <= mex + m0 + m1) {
           sel_bin = 2 * tid + 1;
           sel_n = cex + c0 + c1;
         }
       }
-    } else {
-      const unsigned long long target =
-          static_cast<unsigned long long>(ceil(static_cast<double>(tp) * static_cast<double>(mtot)));
-      if (mex < target && target <= mex + m0) {
-        sel_bin = 2 * tid;
-        sel_n = cex + c0;
-      } else if (mex + m0 < target && target <= mex + m0 + m1) {
-        sel_bin = 2 * tid + 1;
-        sel_n = cex + c0 + c1;
+      __syncthreads();
+      const int tb = sel_bin;
+      const unsigned long long n_list = sel_n;
+      fallback = tb < 0 || tb == kBins - 1 || n_list > static_cast<unsigned long long>(kCand);
+      if (!fallback) {
+        for_chunks(Own{}, [&](const float v[kVec], int64_t base) {
+#pragma unroll
+          for (int j = 0; j < kVec; ++j) {
+            const uint32_t k = order_key(v[j]);
+            append(k >= key_lo && bin_of(v[j]) <= tb, k, v[j], base + j);
+          }
+        });
+        __syncthreads();
+        n = ncand < kCand ? ncand : kCand;  // == n_list
+        listed = true;
       }
     }
-    __syncthreads();
-    const int tb = sel_bin;
-    const unsigned long long n_list = sel_n;
-    fallback = tb < 0 || tb == kBins - 1 || n_list > static_cast<unsigned long long>(kCand);
-    if (!fallback) {
-      // Compaction pass: every kept token at or above the threshold's bin.
-      for (int64_t base = static_cast<int64_t>(tid) * kVec; base < vocab; base += step8) {
-        float v[kVec];
-        x8(v, base);
-#pragma unroll
-        for (int j = 0; j < kVec; ++j) {
-          const uint32_t k = order_key(v[j]);
-          const bool take = k >= key_lo && bin_of(v[j]) <= tb;
-          const unsigned long long bal = __ballot(take);
-          if (bal == 0ull) continue;  // uniform: most slots of most passes
-          const int first = __ffsll(static_cast<long long>(bal)) - 1;
-          int at = 0;
-          if (lane == first) at = atomicAdd(&ncand, __popcll(bal));
-          at = __shfl(at, first, 64) + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
-                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
-          if (take && at < kCand) {
-            ckey[at] = k;
-            cx[at] = v[j];
-          }
-        }
-      }
-      __syncthreads();
-      const int n = ncand < kCand ? ncand : kCand;  // == n_list
-      // top_k on the list: the k-th largest key (ties kept).
-      if (want_k) {
+
+    if (listed) {
+      // top_k on the list: the k-th largest key (ties kept). Every list entry
+      // is kept; a list shorter than k holds every kept token, all of which stay.
+      if (want_k && n >= topk) {
         uint32_t prefix = 0, pmask = 0;
         unsigned long long remaining = static_cast<unsigned long long>(topk);
         for (int shift = 24; shift >= 0; shift -= 8) {
@@ -442,7 +593,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
       }
       // top_p on the list. After top_k the list holds every kept token (its
       // keys >= key_lo), so the kept mass sums over it; top_p alone keeps the
-      // whole row's mass from the histogram pass.
+      // whole row's mass.
       if (want_p) {
         unsigned long long total = mtot;
         if (want_k) {
@@ -558,17 +709,44 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     if (prefix > key_lo) key_lo = prefix;
   }
 
-  // Final pass: kept mass, the draw, the mask bitmap and the support size.
   const uint64_t stream = mix64((a.seeds ? a.seeds[b] : 0ull) + static_cast<uint64_t>(a.step) * 0x9E3779B97F4A7C15ull);
-  float z = 0.f, best = -INFINITY;
+  float best = -INFINITY;
   int64_t bi = 0x7fffffffffffffffll;
   int cnt = 0;
-  for (int64_t c0 = 0; c0 < vocab; c0 += step8) {  // uniform trip count: every lane shuffles below
-    const int64_t base = c0 + static_cast<int64_t>(tid) * kVec;
-    uint32_t bits = 0;
-    if (base < vocab) {
-      float v[kVec];
-      x8(v, base);
+  float lz;  // ln of the kept mass, in units of the maximum's weight
+  if (listed && words <= kMaskWords) {
+    // Final step on the list, which holds every kept token: the kept mass in
+    // fixed point (exact, so independent of the list's order), the draw, the
+    // mask (assembled in LDS) and the support size.
+    if (a.mask)
+      for (int wd = tid; wd < words; wd += kSampleThreads) mbits[wd] = 0u;
+    __syncthreads();
+    unsigned long long zf = 0;
+    for (int i = tid; i < n; i += kSampleThreads) {
+      if (ckey[i] < key_lo) continue;
+      const float x = cx[i];
+      const int64_t t = cidx[i];
+      zf += fixed_mass(x, mx);
+      ++cnt;
+      if (greedy) {
+        arg_better(best, bi, x, t);
+      } else if (x >= mx - kRaceReach) {
+        arg_better(best, bi, x - log_exp_variate(stream, t), t);
+      }
+      if (a.mask) atomicOr(&mbits[t >> 5], 1u << (t & 31));
+    }
+    unsigned long long ztot;
+    (void)block_exscan_u64(zf, red64, ztot);  // its barriers also complete the mask
+    lz = static_cast<float>(log(static_cast<double>(ztot)) - 22.180709777918249);  // - ln 2^32
+    if (a.mask)
+      for (int wd = tid; wd < words; wd += kSampleThreads) a.mask[static_cast<int64_t>(b) * words + wd] = mbits[wd];
+  } else {
+    // Final pass over the row. Every lane makes the same calls (chunks past
+    // the end are all -inf, kept nowhere): the mask words below are assembled
+    // across lanes.
+    float z = 0.f;
+    for_chunks(Every{}, [&](const float v[kVec], int64_t base) {
+      uint32_t bits = 0;
 #pragma unroll
       for (int j = 0; j < kVec; ++j) {
         if (order_key(v[j]) >= key_lo) {
@@ -584,21 +762,21 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
           }
         }
       }
-    }
-    if (a.mask) {
-      // four consecutive lanes hold the 32 bits of one mask word
-      const uint32_t b1 = __shfl_down(bits, 1, 64), b2 = __shfl_down(bits, 2, 64), b3 = __shfl_down(bits, 3, 64);
-      const int64_t wd = base >> 5;
-      if ((tid & 3) == 0 && wd < words)
-        a.mask[static_cast<int64_t>(b) * words + wd] = bits | (b1 << 8) | (b2 << 16) | (b3 << 24);
-    }
+      if (a.mask) {
+        // four consecutive lanes hold the 32 bits of one mask word
+        const uint32_t b1 = __shfl_down(bits, 1, 64), b2 = __shfl_down(bits, 2, 64), b3 = __shfl_down(bits, 3, 64);
+        const int64_t wd = base >> 5;
+        if ((tid & 3) == 0 && wd < words)
+          a.mask[static_cast<int64_t>(b) * words + wd] = bits | (b1 << 8) | (b2 << 16) | (b3 << 24);
+      }
+    });
+    lz = logf(block_sum(z, redv));
   }
-  z = block_sum(z, redv);
   block_argmax(best, bi, redv, redi);
   const float c = block_sum(static_cast<float>(cnt), redv);
   if (tid == 0) {
     a.tokens[b] = bi;
-    if (a.logprobs) a.logprobs[b] = (x_of(bi) - mx) - logf(z);
+    if (a.logprobs) a.logprobs[b] = (x_of(bi) - mx) - lz;
     if (a.counts) a.counts[b] = static_cast<int32_t>(c);
   }
 }
