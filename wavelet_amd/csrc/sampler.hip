@@ -24,9 +24,10 @@ namespace wkv {
 
 constexpr int kSampleThreads = 1024;
 constexpr float kGreedyEps = 1e-5f;  // temperatures below this sample greedily
-// A score x - ln E ranges over [x - 2.812, x + 16.636] (u in [2^-24, 1 - 2^-24]):
-// tokens more than 19.45 below the maximum never win the race (20 leaves margin).
-constexpr float kRaceReach = 20.f;
+// A score x - ln E is at most x + 16.636 (u <= 1 - 2^-24): a token more than
+// kScoreReach below a score already drawn never wins the race (0.064 of margin
+// for float rounding).
+constexpr float kScoreReach = 16.7f;
 
 // Order-preserving key of a float (larger float -> larger key); NaN maps below
 // every real value so it is never kept.
@@ -258,6 +259,8 @@ constexpr int kCand = 4096;
 constexpr int kMassBins = 711;
 // Rows of up to kMaskWords * 32 tokens build their mask in LDS on the list path.
 constexpr int kMaskWords = 8192;
+// Draws a wave may hold back before making them 64 at a time (final pass).
+constexpr int kQueue = 128;
 static_assert(kBins == 2 * kSampleThreads, "the threshold scan gives every thread two bins");
 
 __device__ __forceinline__ unsigned long long fixed_mass(float x, float mx) {
@@ -289,7 +292,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   __shared__ unsigned long long sel_above;
   __shared__ unsigned long long red64[kSampleThreads / 64];
   __shared__ uint32_t fcnt[kBins];
-  __shared__ unsigned long long fmass[kBins];
+  __shared__ unsigned long long fmass[kBins];  // also the final pass's draw queues
+  static_assert(sizeof(fmass) >= (kSampleThreads / 64) * kQueue * 8, "the draw queues fit the mass bins");
   __shared__ uint32_t ckey[kCand];
   __shared__ float cx[kCand];
   __shared__ int32_t cidx[kCand];
@@ -364,12 +368,31 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   using Every = std::true_type;
   using Own = std::false_type;
 
-  // Pass 1: the row maximum; each thread keeps its own (top_k's capture range).
+  // Pass 1: the row maximum. Each thread keeps its own (top_k's capture range)
+  // and, for rows drawn by the full-row pass, where it is (the race's bound).
+  const int topk = a.top_k ? a.top_k[b] : 0;
+  const float tp = a.top_p ? a.top_p[b] : 1.f;
+  const bool want_k = topk > 0 && topk < vocab;
+  const bool want_p = tp < 1.f;
+  const bool track = !greedy && !want_k && !want_p;
   float tmx = -INFINITY;
-  for_chunks(Own{}, [&](const float v[kVec], int64_t) {
+  int tmi = 0;
+  if (track) {
+    for_chunks(Own{}, [&](const float v[kVec], int64_t base) {
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) tmx = fmaxf(tmx, v[j]);  // NaN never wins
-  });
+      for (int j = 0; j < kVec; ++j) {
+        if (v[j] > tmx) {  // NaN never wins
+          tmx = v[j];
+          tmi = static_cast<int>(base) + j;
+        }
+      }
+    });
+  } else {
+    for_chunks(Own{}, [&](const float v[kVec], int64_t) {
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) tmx = fmaxf(tmx, v[j]);  // NaN never wins
+    });
+  }
   const float mx = block_max(tmx, redv);
   if (!(mx > -INFINITY)) {  // nothing finite: token 0, empty support
     if (tid == 0) {
@@ -389,10 +412,6 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     key_lo = k > key_lo ? k : key_lo;
   }
 
-  const int topk = a.top_k ? a.top_k[b] : 0;
-  const float tp = a.top_p ? a.top_p[b] : 1.f;
-  const bool want_k = topk > 0 && topk < vocab;
-  const bool want_p = tp < 1.f;
   const int lane = tid & 63;
   bool fallback = false;
   bool listed = false;  // the LDS list holds every kept token the threshold can keep
@@ -714,6 +733,28 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   int64_t bi = 0x7fffffffffffffffll;
   int cnt = 0;
   float lz;  // ln of the kept mass, in units of the maximum's weight
+  // The race's bound, raised by each thread's own draws as they come: a
+  // token below bound - kScoreReach cannot reach it, so its draw is skipped.
+  // It starts from the maximum's least possible score (ln E <= 2.812; the
+  // maximum is always kept), or from the best score of the threads' kept
+  // maxima where pass 1 kept them.
+  float lim = -INFINITY;
+  if (!greedy) {
+    lim = mx - 2.9f;
+    if (track) {
+      const float s0 = order_key(tmx) >= key_lo ? tmx - log_exp_variate(stream, tmi) : -INFINITY;
+      lim = fmaxf(lim, block_max(s0, redv));
+    }
+    lim -= kScoreReach;
+  }
+  auto race = [&](float x, int64_t t) {
+    if (greedy) {
+      arg_better(best, bi, x, t);
+    } else if (x >= lim) {
+      arg_better(best, bi, x - log_exp_variate(stream, t), t);
+      lim = fmaxf(lim, best - kScoreReach);
+    }
+  };
   if (listed && words <= kMaskWords) {
     // Final step on the list, which holds every kept token: the kept mass in
     // fixed point (exact, so independent of the list's order), the draw, the
@@ -728,11 +769,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
       const int64_t t = cidx[i];
       zf += fixed_mass(x, mx);
       ++cnt;
-      if (greedy) {
-        arg_better(best, bi, x, t);
-      } else if (x >= mx - kRaceReach) {
-        arg_better(best, bi, x - log_exp_variate(stream, t), t);
-      }
+      race(x, t);
       if (a.mask) atomicOr(&mbits[t >> 5], 1u << (t & 31));
     }
     unsigned long long ztot;
@@ -744,24 +781,43 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     // Final pass over the row. Every lane makes the same calls (chunks past
     // the end are all -inf, kept nowhere): the mask words below are assembled
     // across lanes.
+    // The draws go through a queue per wave (in the top_p mass bins, idle by
+    // now) and are made 64 at a time, one per lane: a draw taken in place would
+    // hold the whole wave whenever any one lane needs it.
+    float *qx = reinterpret_cast<float *>(fmass) + (tid >> 6) * (2 * kQueue);
+    int32_t *qt = reinterpret_cast<int32_t *>(qx + kQueue);
+    int qn = 0;  // wave-uniform
     float z = 0.f;
     for_chunks(Every{}, [&](const float v[kVec], int64_t base) {
       uint32_t bits = 0;
 #pragma unroll
       for (int j = 0; j < kVec; ++j) {
-        if (order_key(v[j]) >= key_lo) {
+        const bool kept = order_key(v[j]) >= key_lo;
+        if (__ballot(kept) == 0ull) continue;  // uniform: nothing kept in this slot of the wave
+        if (kept) {
           bits |= 1u << j;
-          z += expf(v[j] - mx);
-          ++cnt;
-          // ln E lies in [-16.64, 2.82], so a token below mx - kRaceReach scores
-          // under the maximum's least possible score and cannot win: its draw is skipped.
-          if (greedy) {
-            arg_better(best, bi, v[j], base + j);
-          } else if (v[j] >= mx - kRaceReach) {
-            arg_better(best, bi, v[j] - log_exp_variate(stream, base + j), base + j);
-          }
+          z += __expf(v[j] - mx);  // (relative error ~1e-6 at 100 below the maximum)
+        }
+        if (greedy) {
+          if (kept) arg_better(best, bi, v[j], base + j);
+          continue;
+        }
+        const bool c = kept && v[j] >= lim;
+        const unsigned long long bal = __ballot(c);
+        if (bal == 0ull) continue;  // uniform
+        if (c) {
+          const int at = qn + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                  static_cast<uint32_t>(bal >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+          qx[at] = v[j];
+          qt[at] = static_cast<int32_t>(base) + j;
+        }
+        qn += __popcll(bal);  // < 64 before, < 128 after
+        if (qn >= 64) {
+          qn -= 64;
+          race(qx[qn + lane], qt[qn + lane]);
         }
       }
+      cnt += __popc(bits);
       if (a.mask) {
         // four consecutive lanes hold the 32 bits of one mask word
         const uint32_t b1 = __shfl_down(bits, 1, 64), b2 = __shfl_down(bits, 2, 64), b3 = __shfl_down(bits, 3, 64);
@@ -770,6 +826,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
           a.mask[static_cast<int64_t>(b) * words + wd] = bits | (b1 << 8) | (b2 << 16) | (b3 << 24);
       }
     });
+    if (lane < qn) race(qx[lane], qt[lane]);
     lz = logf(block_sum(z, redv));
   }
   block_argmax(best, bi, redv, redi);
