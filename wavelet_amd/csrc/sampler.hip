@@ -483,20 +483,40 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
       }
     }
 
-    // Capture pass: the kept tokens within the range go to the list; the
-    // kept mass sums over the whole row (a token kMassBins or more below the
-    // maximum weighs under one fixed-point unit: exactly 0).
-    if (bcap < kBins - 1) {
+    // Capture pass: the kept tokens within the range go to the list and to
+    // the threshold's histogram (for a list that overflows); the kept mass
+    // sums over the whole row (a token kMassBins or more below the maximum
+    // weighs under one fixed-point unit: exactly 0).
+    const bool captured = bcap < kBins - 1;
+    if (captured) {
       unsigned long long tmass = 0;
-      for_chunks(Own{}, [&](const float v[kVec], int64_t base) {
+      // (one instance per mass flag: a select on it would compute every mass)
+      auto capture = [&](auto with_mass) {
+        constexpr bool M = decltype(with_mass)::value;
+        for_chunks(Own{}, [&](const float v[kVec], int64_t base) {
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) {
-          const uint32_t k = order_key(v[j]);
-          const int bn = bin_of(v[j]);
-          if (hmass && k >= key_lo && bn < kMassBins) tmass += fixed_mass(v[j], mx);
-          append(k >= key_lo && bn <= bcap, k, v[j], base + j);
-        }
-      });
+          for (int j = 0; j < kVec; ++j) {
+            const uint32_t k = order_key(v[j]);
+            const int bn = bin_of(v[j]);
+            const bool kept = k >= key_lo;
+            unsigned long long m = 0;
+            if constexpr (M) {
+              if (kept && bn < kMassBins) m = fixed_mass(v[j], mx);
+              tmass += m;
+            }
+            const bool take = kept && bn <= bcap;
+            if (take) {
+              atomicAdd(&fcnt[bn], 1u);
+              if constexpr (M) atomicAdd(&fmass[bn], m);
+            }
+            append(take, k, v[j], base + j);
+          }
+        });
+      };
+      if (hmass)
+        capture(std::true_type{});
+      else
+        capture(std::false_type{});
       if (hmass) {
         const unsigned long long wm = wave_sum_u64(tmass);
         if (lane == 0) atomicAdd(&sel_n, wm);
@@ -509,30 +529,33 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     }
 
     if (!listed) {
-      // Histogram pass over the whole row, then a compaction pass: every kept
-      // token at or above the threshold's bin.
+      // The threshold's bin from the histogram -- the capture pass's, which
+      // holds the threshold, or one pass over the whole row -- then a
+      // compaction pass: every kept token at or above that bin.
       if (tid == 0) ncand = 0;
-      uint32_t tcnt = 0;
-      unsigned long long tmass = 0;  // this thread's share of the open bin
-      for_chunks(Own{}, [&](const float v[kVec], int64_t) {
+      if (!captured) {
+        uint32_t tcnt = 0;
+        unsigned long long tmass = 0;  // this thread's share of the open bin
+        for_chunks(Own{}, [&](const float v[kVec], int64_t) {
 #pragma unroll
-        for (int j = 0; j < kVec; ++j) {
-          if (order_key(v[j]) < key_lo) continue;
-          const int bn = bin_of(v[j]);
-          const unsigned long long m = hmass ? fixed_mass(v[j], mx) : 0ull;
-          if (bn == kBins - 1) {
-            ++tcnt;
-            tmass += m;
-          } else {
-            atomicAdd(&fcnt[bn], 1u);
-            if (hmass) atomicAdd(&fmass[bn], m);
+          for (int j = 0; j < kVec; ++j) {
+            if (order_key(v[j]) < key_lo) continue;
+            const int bn = bin_of(v[j]);
+            const unsigned long long m = hmass ? fixed_mass(v[j], mx) : 0ull;
+            if (bn == kBins - 1) {
+              ++tcnt;
+              tmass += m;
+            } else {
+              atomicAdd(&fcnt[bn], 1u);
+              if (hmass) atomicAdd(&fmass[bn], m);
+            }
           }
+        });
+        const unsigned long long wc = wave_sum_u64(tcnt), wm = wave_sum_u64(tmass);
+        if (lane == 0) {
+          atomicAdd(&fcnt[kBins - 1], static_cast<uint32_t>(wc));
+          if (hmass) atomicAdd(&fmass[kBins - 1], wm);
         }
-      });
-      const unsigned long long wc = wave_sum_u64(tcnt), wm = wave_sum_u64(tmass);
-      if (lane == 0) {
-        atomicAdd(&fcnt[kBins - 1], static_cast<uint32_t>(wc));
-        if (hmass) atomicAdd(&fmass[kBins - 1], wm);
       }
       __syncthreads();
       // Threshold bin from scans over the bins in value order (bin 0 = nearest the max).
@@ -543,7 +566,9 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
       if (hmass) {
         m0 = fmass[2 * tid];
         m1 = fmass[2 * tid + 1];
-        mex = block_exscan_u64(m0 + m1, red64, mtot);
+        unsigned long long htot;
+        mex = block_exscan_u64(m0 + m1, red64, htot);
+        if (!captured) mtot = htot;  // else the capture pass summed the whole row
       }
       if (tid == 0) sel_bin = -1;
       __syncthreads();
