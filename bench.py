@@ -38,7 +38,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="qwen3-4b",
                     choices=["qwen3-4b", "qwen3-4b-var", "qwen2.5-0.5b", "qwen2.5-7b-groups", "deepseek-v3-mla",
-                             "qwen3-4b-prefill", "sampler"],
+                             "qwen3-4b-prefill", "sampler", "sampler-default"],
                     help="qwen3-4b is the headline; the others are the remaining measured shapes")
     ap.add_argument("--layers", type=int, default=0, help="0 = the model's depth (8 rotated layers for MLA)")
     ap.add_argument("--batch", type=int, default=64)
@@ -291,15 +291,24 @@ def workload(args, torch, dev) -> dict:
                 "flops_per_layer": flops, "cache_bytes": caches[0].nbytes, "bound": "mfma",
                 "desc": f"Qwen3-4B prompt step: {args.layers} layers x (append + causal prefill attention), "
                         f"{B} prompts x {n_new} tokens, 32 q / 8 kv heads, d=128, bf16, block 16"}
-    elif name == "sampler":
-        # the step after decode: one token per row from bf16 logits over Qwen's vocabulary,
-        # temperature 0.7, top_k 50, top_p 0.9, with processed logprobs and the sampling mask
+    elif name in ("sampler", "sampler-default"):
+        # the step after decode: one token per row from bf16 logits over Qwen's vocabulary with
+        # processed logprobs and the sampling mask; "sampler": temperature 0.7, top_k 50, top_p 0.9;
+        # "sampler-default": the RL sampling defaults (temperature 1, top_p 1, top_k and min_p off,
+        # configs/config.py:854-859), which draw from the whole row
         from wavelet_amd import sample
-
         B, V = 256, 151936
+        # per-row parameter tensors and outputs made once, as a serving loop keeps them
+        per_row = ({"temperature": (0.7, torch.float32), "top_k": (50, torch.int32), "top_p": (0.9, torch.float32)}
+                   if name == "sampler" else {"temperature": (1.0, torch.float32)})
+        params = {k: torch.full((B,), v, dtype=dt, device=dev) for k, (v, dt) in per_row.items()}
+        outs = (torch.empty(B, dtype=torch.int64, device=dev), torch.empty(B, dtype=torch.float32, device=dev),
+                torch.empty((B, (V + 31) // 32), dtype=torch.int32, device=dev),
+                torch.empty(B, dtype=torch.int32, device=dev))
         gen = torch.Generator(device=dev)
         gen.manual_seed(1234)
-        logits = (torch.randn((B, V), generator=gen, device=dev) * 4).to(torch.bfloat16)
+        # four logits buffers in turn (311 MB, beyond the 256 MB last-level cache): no call re-reads a cached row
+        logits = [(torch.randn((B, V), generator=gen, device=dev) * 4).to(torch.bfloat16) for _ in range(4)]
         seeds = torch.arange(B, dtype=torch.int64, device=dev)
 
         class _Step:
@@ -310,7 +319,7 @@ def workload(args, torch, dev) -> dict:
 
             def step_layer(self, layer):
                 self.n += 1
-                sample(logits, temperature=0.7, top_k=50, top_p=0.9, seeds=seeds, step=self.n, return_mask=True)
+                sample(logits[self.n % 4], seeds=seeds, step=self.n, return_mask=True, out=outs, **params)
 
             def run(self):
                 self.step_layer(0)
@@ -323,9 +332,10 @@ def workload(args, torch, dev) -> dict:
         return {"name": name, "step": _Step(), "w": w, "layer_bytes": nbytes, "attn_bytes": nbytes, "split": False,
                 "kernel": "sample_kernel<bf16>", "dtype": "bf16 logits, fp32 math", "flops_per_layer": 0,
                 "metric": "sampler GB/s of logits & us/step, 256 x 151936",
-                "cache_bytes": B * V * 2,
-                "desc": f"token sampler: {B} rows x {V} bf16 logits, T=0.7, top_k=50, top_p=0.9, processed "
-                        "logprobs + sampling mask"}
+                "cache_bytes": 4 * B * V * 2,
+                "desc": f"token sampler: {B} rows x {V} bf16 logits, "
+                        + ("T=0.7, top_k=50, top_p=0.9" if name == "sampler" else "T=1, top_p=1, no top_k / min_p")
+                        + ", processed logprobs + sampling mask"}
     else:
         raise SystemExit(f"unknown workload {name}")
     L = w.context_lens.astype(np.int64)
@@ -383,14 +393,16 @@ def main() -> int:
     def per_launch(fn, reps):
         # one event pair around each pass of back-to-back launches over all layers:
         # the mean device time per layer call, without a gap per launch
+        # (at least 8 launches a pass: one pass of a one-launch step would time the host's launch gap)
+        n = max(args.layers, 8)
         pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
         for a, b in pairs:
             a.record()
-            for layer in range(args.layers):
-                fn(layer)
+            for i in range(n):
+                fn(i % args.layers)
             b.record()
         torch.cuda.synchronize()
-        return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3 / args.layers
+        return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3 / n
 
     kernel_us = per_launch(step.step_layer, args.kernel_reps)
     split = wl.get("split", True)  # the step has separate append and attention calls

@@ -146,3 +146,21 @@ def test_sampler_edge_rows(cuda):
     assert tok[0] == 123 and abs(lp[0]) < 1e-6 and counts[0] == 1
     assert tok[1] == 7 and counts[1] == V
     assert counts[2] == 10 and tok[2] < 10
+
+
+def test_sampler_out_buffers(cuda):
+    """Preallocated outputs give the same results; wrong shapes or dtypes are rejected."""
+    B, V = 4, 5000
+    x = torch.from_numpy((synth.normal(synth.stream_key("smp-out"), B * V) * 3.0).astype(np.float32).reshape(B, V)).to(cuda)
+    seeds = torch.arange(B, dtype=torch.int64, device=cuda)
+    ref = sample(x, temperature=0.8, top_k=20, seeds=seeds, step=3, return_mask=True)
+    words = (V + 31) // 32
+    out = (torch.empty(B, dtype=torch.int64, device=cuda), torch.empty(B, dtype=torch.float32, device=cuda),
+           torch.empty((B, words), dtype=torch.int32, device=cuda), torch.empty(B, dtype=torch.int32, device=cuda))
+    got = sample(x, temperature=0.8, top_k=20, seeds=seeds, step=3, return_mask=True, out=out)
+    for r, g, o in zip(ref, got, out):
+        assert g is o and torch.equal(r, g)
+    with pytest.raises(ValueError, match="mask"):
+        sample(x, return_mask=True, out=(out[0], out[1], None, out[3]))
+    with pytest.raises(ValueError, match="logprobs"):
+        sample(x, out=(out[0], out[1].double(), None, None))

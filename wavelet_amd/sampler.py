@@ -44,6 +44,7 @@ def sample(
     seeds: torch.Tensor | None = None,
     step: int = 0,
     return_mask: bool = False,
+    out=None,
 ):
     """Sample one token per row of ``logits [B, V]`` (fp32 or bf16).
 
@@ -53,7 +54,9 @@ def sample(
     int64 and ``step`` fix the random stream. Returns ``(tokens [B] int64,
     logprobs [B] fp32, mask, counts)``; ``mask`` is the ``[B, ceil(V/32)]``
     int32 bitmap of the kept set (``mask_token_ids`` lists it) and ``counts``
-    its sizes, both ``None`` unless ``return_mask``.
+    its sizes, both ``None`` unless ``return_mask``. ``out`` may hold those four
+    outputs, preallocated (mask and counts may be ``None`` without
+    ``return_mask``): a serving loop then allocates nothing per step.
     """
     if logits.dim() != 2 or logits.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("logits must be a float32 or bfloat16 [B, V] tensor")
@@ -63,10 +66,25 @@ def sample(
         logits = logits.contiguous()
     batch, vocab = logits.shape
     words = (vocab + 31) // 32
-    tokens = torch.empty(batch, dtype=torch.int64, device=dev)
-    logprobs = torch.empty(batch, dtype=torch.float32, device=dev)
-    mask = torch.empty((batch, words), dtype=torch.int32, device=dev) if return_mask else None
-    counts = torch.empty(batch, dtype=torch.int32, device=dev) if return_mask else None
+    if out is None:
+        tokens = torch.empty(batch, dtype=torch.int64, device=dev)
+        logprobs = torch.empty(batch, dtype=torch.float32, device=dev)
+        mask = torch.empty((batch, words), dtype=torch.int32, device=dev) if return_mask else None
+        counts = torch.empty(batch, dtype=torch.int32, device=dev) if return_mask else None
+    else:
+        tokens, logprobs, mask, counts = out
+        for x, name, dt, shape in ((tokens, "tokens", torch.int64, (batch,)), (logprobs, "logprobs", torch.float32,
+                                   (batch,)), (mask, "mask", torch.int32, (batch, words)),
+                                   (counts, "counts", torch.int32, (batch,))):
+            if x is None:
+                if return_mask and name in ("mask", "counts"):
+                    raise ValueError(f"out: {name} is needed with return_mask")
+                continue
+            _require_cuda(x, f"out {name}", dev)
+            if x.dtype != dt or tuple(x.shape) != shape or not x.is_contiguous():
+                raise ValueError(f"out: {name} must be a contiguous {dt} tensor of shape {shape}")
+        if not return_mask:
+            mask = counts = None
     if batch == 0:
         return tokens, logprobs, mask, counts
     t = _per_row(temperature, "temperature", batch, torch.float32, dev)
