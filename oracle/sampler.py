@@ -47,6 +47,9 @@ def log_exp_variates(seed: int, step: int, n: int) -> np.ndarray:
     # 23 hash bits: u in [2^-24, 1 - 2^-24], exact in float32 (with 24 bits the
     # top value rounds to 1.0, giving E = 0 and an infinite race score)
     u = ((h >> np.uint64(41)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 8388608.0)
+    # (the kernel takes both logarithms as the hardware log2 times ln 2: within an
+    # ulp or two of these, so race scores agree to ~1e-6 and only near-ties of
+    # the race may pick another token)
     return np.log(-np.log(u)).astype(np.float32)
 
 

@@ -46,11 +46,18 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 
 // ln(E) of the Exp(1) variate of token i: u in [2^-24, 1 - 2^-24] from 23
 // hash bits, exact in float32 (24 bits would round the top value to 1.0:
-// E = 0 and an infinite race score for one token in 2^24).
+// E = 0 and an infinite race score for one token in 2^24). Both logarithms
+// take the hardware log2 times ln 2: their arguments (u >= 2^-24, -ln u >=
+// 6e-8) are never denormal, so logf's scaling and extended-precision fixups
+// buy at most an ulp here.
 __device__ __forceinline__ float log_exp_variate(uint64_t stream, int64_t i) {
   const uint64_t h = mix64(stream + static_cast<uint64_t>(i));
-  const float u = (static_cast<float>(h >> 41) + 0.5f) * (1.0f / 8388608.0f);
-  return logf(-logf(u));
+  // u = (m + 0.5) 2^-23 for the top 23 bits m, exactly: 1 + m 2^-23 from the
+  // bits, minus 1 (exact), plus 2^-24 (exact at that magnitude).
+  const uint32_t m = static_cast<uint32_t>(h >> 32) >> 9;
+  const float u = (__uint_as_float(0x3F800000u | m) - 1.0f) + 5.9604644775390625e-8f;
+  constexpr float kLn2 = 0.693147180559945309f;
+  return __builtin_amdgcn_logf(-__builtin_amdgcn_logf(u) * kLn2) * kLn2;
 }
 
 template <typename T>
