@@ -82,8 +82,8 @@ def sample_row(logits, *, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repeti
     mx = np.float32(x[finite].max())
     keys = order_key(x)
     key_lo = order_key(np.float32(-3.402823466e38))
-    if min_p > 0:
-        key_lo = max(key_lo, order_key(np.float32(mx + np.float32(np.log(np.float32(min_p))))))
+    if min_p > 0:  # (capped at the maximum's key: min_p above 1 still keeps the maximum)
+        key_lo = max(key_lo, min(order_key(np.float32(mx + np.float32(np.log(np.float32(min_p))))), order_key(mx)))
     v = x.size
     if 0 < top_k < v:
         kk = _radix_key_topk(keys[keys >= key_lo], int(top_k))

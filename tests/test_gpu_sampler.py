@@ -164,3 +164,19 @@ def test_sampler_out_buffers(cuda):
         sample(x, return_mask=True, out=(out[0], out[1], None, out[3]))
     with pytest.raises(ValueError, match="logprobs"):
         sample(x, out=(out[0], out[1].double(), None, None))
+
+
+def test_sampler_parameter_ranges(cuda):
+    """Scalars outside the sampling config's ranges are rejected; a per-row min_p above 1 (not read
+    back) keeps the row's maximum, as min_p = 1 does."""
+    V = 2000
+    x = (synth.normal(synth.stream_key("smp-ranges"), 2 * V) * 3.0).astype(np.float32).reshape(2, V)
+    logits = torch.from_numpy(x).to(cuda)
+    for kw in (dict(min_p=1.5), dict(min_p=-0.1), dict(top_p=0.0), dict(top_p=1.2), dict(temperature=-1.0),
+               dict(repetition_penalty=0.0)):
+        with pytest.raises(ValueError):
+            sample(logits, **kw)
+    rows = [(1.0, 0, 1.0, 2.0, 1.0), (0.7, 5, 1.0, 1.0, 1.0)]
+    _check_rows(cuda, x, rows, [np.zeros(0, np.int64)] * 2, np.arange(2, dtype=np.int64), 1, torch.float32)
+    tok = sample(logits, min_p=torch.tensor([2.0, 2.0], device=cuda))[0].cpu().numpy()
+    np.testing.assert_array_equal(tok, np.argmax(x, axis=1))

@@ -97,3 +97,10 @@ def test_uniform_stays_inside_the_open_interval():
     assert float(u24) == 1.0  # the mapping this replaced
     v = S.log_exp_variates(seed=123, step=7, n=200_000)
     assert np.all(np.isfinite(v))
+
+
+def test_min_p_above_one_keeps_the_maximum():
+    x = np.array([0.5, 2.0, -1.0, 2.0, 1.9], np.float32)
+    tok, lp, kept, _ = S.sample_row(x, min_p=3.0, seed=1, step=0)
+    np.testing.assert_array_equal(kept, [False, True, False, True, False])  # the tied maxima
+    assert tok in (1, 3) and abs(lp - np.log(0.5)) < 1e-6

@@ -415,7 +415,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   const float mp = a.min_p ? a.min_p[b] : 0.f;
   uint32_t key_lo = order_key(-3.402823466e38f);  // finite values only
   if (mp > 0.f) {
-    const uint32_t k = order_key(mx + logf(mp));
+    uint32_t k = order_key(mx + logf(mp));
+    if (k > order_key(mx)) k = order_key(mx);  // min_p above 1 still keeps the maximum
     key_lo = k > key_lo ? k : key_lo;
   }
 

@@ -19,9 +19,24 @@ from . import _lib
 from .cache import _require_cuda, _stream
 
 
+# Ranges a scalar parameter must lie in (the reference's sampling config:
+# configs/config.py:854-859); per-row tensors are not read back (that would
+# synchronise): the kernel keeps at least the row's maximum whatever min_p is.
+_RANGES = {
+    "temperature": (lambda x: x >= 0.0, ">= 0"),
+    "top_p": (lambda x: 0.0 < x <= 1.0, "in (0, 1]"),
+    "min_p": (lambda x: 0.0 <= x <= 1.0, "in [0, 1]"),
+    "repetition_penalty": (lambda x: x > 0.0, "> 0"),
+}
+
+
 def _per_row(v, name: str, batch: int, dtype: torch.dtype, device: torch.device):
     if v is None:
         return None
+    if not isinstance(v, torch.Tensor) and name in _RANGES:
+        ok, text = _RANGES[name]
+        if not ok(float(v)):
+            raise ValueError(f"{name} must be {text} (got {v})")
     if isinstance(v, torch.Tensor):
         _require_cuda(v, name, device)
         if v.dim() == 0:
