@@ -5,6 +5,7 @@ softmax it must draw from, greedy rows, penalties and logprobs."""
 import math
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import sampler as S
@@ -104,3 +105,12 @@ def test_min_p_above_one_keeps_the_maximum():
     tok, lp, kept, _ = S.sample_row(x, min_p=3.0, seed=1, step=0)
     np.testing.assert_array_equal(kept, [False, True, False, True, False])  # the tied maxima
     assert tok in (1, 3) and abs(lp - np.log(0.5)) < 1e-6
+
+
+@pytest.mark.parametrize("kw", [dict(min_p=1.5), dict(min_p=-0.1), dict(top_p=0.0), dict(top_p=1.2),
+                                dict(temperature=-1.0), dict(repetition_penalty=0.0)])
+def test_sample_rejects_out_of_range_scalars(kw):
+    """Checked on the host before anything touches a device (the reference config's ranges)."""
+    from wavelet_amd import sample
+    with pytest.raises(ValueError, match=next(iter(kw))):
+        sample(torch.zeros((2, 10)), **kw)

@@ -30,13 +30,16 @@ _RANGES = {
 }
 
 
-def _per_row(v, name: str, batch: int, dtype: torch.dtype, device: torch.device):
-    if v is None:
-        return None
-    if not isinstance(v, torch.Tensor) and name in _RANGES:
+def _check_scalar(name: str, v) -> None:
+    if v is not None and not isinstance(v, torch.Tensor) and name in _RANGES:
         ok, text = _RANGES[name]
         if not ok(float(v)):
             raise ValueError(f"{name} must be {text} (got {v})")
+
+
+def _per_row(v, name: str, batch: int, dtype: torch.dtype, device: torch.device):
+    if v is None:
+        return None
     if isinstance(v, torch.Tensor):
         _require_cuda(v, name, device)
         if v.dim() == 0:
@@ -73,6 +76,9 @@ def sample(
     outputs, preallocated (mask and counts may be ``None`` without
     ``return_mask``): a serving loop then allocates nothing per step.
     """
+    for name, v in (("temperature", temperature), ("top_p", top_p), ("min_p", min_p),
+                    ("repetition_penalty", repetition_penalty)):
+        _check_scalar(name, v)
     if logits.dim() != 2 or logits.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("logits must be a float32 or bfloat16 [B, V] tensor")
     dev = logits.device
