@@ -23,6 +23,8 @@
 #include "gqa_tiles.h"
 #include "lds_dma.h"
 
+#include <type_traits>
+
 namespace wkv {
 
 constexpr int kPrefillWaves = 4;
@@ -66,7 +68,82 @@ __device__ __forceinline__ const uint8_t *tile_piece(const uint8_t *kc, const ui
   return vc + rbase + (static_cast<int64_t>(d) * BS + o0) * T::ESZ + half * 16;
 }
 
-constexpr int kPrefillBufs = 3;  // LDS tile buffers: one attended, two in flight
+// LDS tile buffers: fp8, one attended and two in flight; bf16, a pair
+// attended and the next pair in flight.
+template <bool FP8>
+constexpr int prefill_bufs() {
+  return FP8 ? 3 : 4;
+}
+
+// Zeroes the bf16 V values of the tile slots at or past `valid` (4 tokens
+// 4 grp .. 4 grp + 3 of one d row): a slot outside the sequence may hold NaN.
+__device__ __forceinline__ u32x2 mask_v4(u32x2 v, int valid, int grp) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (4 * grp + e >= valid) v[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+  return v;
+}
+
+// Two 16-key tiles of bf16 online-softmax attention at once: one row maximum,
+// one rescale test, and the PV products as 16x16x32 MFMAs over the 32 keys --
+// half the PV instructions of two 16-key steps. The PV product's k slots
+// 8 grp .. 8 grp + 3 hold tile a's keys 4 grp .. 4 grp + 3 and slots
+// 8 grp + 4 .. 8 grp + 7 tile b's: P and V are packed the same way, and the
+// sum over k does not depend on which key a slot carries. lim_a / lim_b: the
+// keys of each tile this lane's column sees (0..16, the causal diagonal). The
+// V operands are read from the tiles' LDS copies (lva, lvb) as each PV
+// product needs them, so they are not held through the softmax.
+template <int D>
+__device__ __forceinline__ void attend_pair(DecodeState<D, false> &st, const Tile<D, false> &ta,
+                                            const Tile<D, false> &tb, const uint8_t *lva, const uint8_t *lvb,
+                                            const bf16x8 *qop, float scale_log2, int col, int grp, int lim_a,
+                                            int lim_b) {
+  floatx4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) {
+    sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ta.k[j]), qop[j], sa, 0, 0, 0);
+    sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, tb.k[j]), qop[j], sb, 0, 0, 0);
+  }
+  const int ca = ta.valid < lim_a ? ta.valid : lim_a;
+  const int cb = tb.valid < lim_b ? tb.valid : lim_b;
+  float sv[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sv[i] = 4 * grp + i < ca ? sa[i] * scale_log2 : -INFINITY;
+    sv[4 + i] = 4 * grp + i < cb ? sb[i] * scale_log2 : -INFINITY;
+  }
+  const float mt = row_max4(fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                                  fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))));
+  // st.m is the reference maximum (-inf until the first attended token).
+  const bool move = mt > st.m + SOFTMAX_TAU;
+  const float m_new = move ? mt : st.m;
+  const float corr = (move && st.m != -INFINITY) ? fast_exp2(st.m - m_new) : 1.f;
+  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
+  st.l = st.l * corr + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+  st.m = m_new;
+  if (__any(corr != 1.f)) {  // a reference maximum moved for some head: rescale
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st.o[n][i] *= corr;
+    }
+  }
+  const u32x4 pb = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                    pack_bf16x2(p[6], p[7])};
+  const bf16x8 pop = __builtin_bit_cast(bf16x8, pb);
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) {
+    const int off = ((grp >> 1) * D + 16 * n + col) * 16 + (grp & 1) * 8;
+    u32x2 va = *reinterpret_cast<const u32x2 *>(lva + off), vb = *reinterpret_cast<const u32x2 *>(lvb + off);
+    if (ta.valid < 16) va = mask_v4(va, ta.valid, grp);  // uniform: a partial tile
+    if (tb.valid < 16) vb = mask_v4(vb, tb.valid, grp);
+    const u32x4 v8 = {va[0], va[1], vb[0], vb[1]};
+    st.o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, v8), pop, st.o[n], 0, 0, 0);
+  }
+}
 
 template <int D, bool FP8>
 __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
@@ -76,7 +153,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
     const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
     int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
   using LT = LdsTile<D, FP8>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kPrefillBufs][LT::BYTES];
+  constexpr int NBUF = prefill_bufs<FP8>();
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][LT::BYTES];
   // Linear id = ((item / 8) * n_qt + (n_qt - 1 - qt)) * 8 + item % 8, item =
   // (sequence, KV head, head group): the XCD (id % 8) depends on the item only.
   const int id = blockIdx.x;
@@ -140,8 +218,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
   // into the buffer tile i - 1 left; before the barrier that publishes tile
   // i + 1 each wave waits for its own copies of it.
   const int wave_base = 64 * wave;
-  int okr[kPrefillBufs];
-  float kscr[kPrefillBufs], vscr[kPrefillBufs];
+  int okr[NBUF];
+  float kscr[NBUF], vscr[NBUF];
   auto issue = [&](int i, int bi) {
     int64_t rbase;
     int o0;
@@ -155,8 +233,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
                       __builtin_amdgcn_readfirstlane(dst + 16 * p0));
     }
   };
-  auto attend = [&](int i, int bi) {
-    Tile<D, FP8> t;
+  // Tile i from LDS buffer bi into registers (V too unless !WITH_V); its
+  // column limit in `lim`.
+  auto read_tile = [&](int i, int bi, Tile<D, FP8> &t, int &lim, auto with_v) {
     const uint8_t *lk = &lds[bi][0];
     const uint8_t *lv = &lds[bi][LT::KB];
 #pragma unroll
@@ -166,22 +245,52 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
 #pragma unroll
       for (int j = 0; j < Tile<D, FP8>::NPV / 4; ++j)
         t.v4[j] = *reinterpret_cast<const u32x4 *>(lv + (64 * j + 16 * grp + col) * 16);
-    } else {
+    } else if constexpr (decltype(with_v)::value) {
 #pragma unroll
       for (int n = 0; n < Tile<D, FP8>::NPV; ++n)
         t.v[n] = *reinterpret_cast<const u32x2 *>(lv + ((grp >> 1) * D + 16 * n + col) * 16 + (grp & 1) * 8);
     }
     const int ts = 16 * i;
     t.ts = ts;
-    t.valid = okr[bi] ? ((kend - ts) < 16 ? (kend - ts) : 16) : 0;
+    t.valid = (i < n_tiles && okr[bi]) ? ((kend - ts) < 16 ? (kend - ts) : 16) : 0;
     t.ksc = kscr[bi];
     t.vsc = vscr[bi];
-    int lim = pos - ts + 1;  // keys of the tile this column sees
+    lim = pos - ts + 1;  // keys of the tile this column sees
     lim = lim < 0 ? 0 : (lim > 16 ? 16 : lim);
+  };
+  auto attend = [&](int i, int bi) {
+    Tile<D, FP8> t;
+    int lim;
+    read_tile(i, bi, t, lim, std::true_type{});
     if (t.valid > 0) attend_tile<D, FP8, true>(st, t, qop, scale_log2, grp, lim);
   };
 
-  if (n_tiles > 0) {
+  if constexpr (!FP8) {
+    // bf16: tiles in pairs. Pair j sits in buffers 2 (j & 1), +1; the next
+    // pair's copies go out before this one is attended (its buffers were left
+    // by pair j - 1 at the last barrier) and land before the next barrier.
+    if (n_tiles > 0) {
+      issue(0, 0);
+      if (n_tiles > 1) issue(1, 1);
+      wait_vmcnt<0>();
+      barrier_lds();
+      for (int j = 0; 2 * j < n_tiles; ++j) {
+        const int cur = 2 * (j & 1), nxt = 2 - cur;
+        if (2 * j + 2 < n_tiles) issue(2 * j + 2, nxt);
+        if (2 * j + 3 < n_tiles) issue(2 * j + 3, nxt + 1);
+        if (active) {
+          Tile<D, FP8> ta, tb;
+          int la, lb;
+          read_tile(2 * j, cur, ta, la, std::false_type{});
+          read_tile(2 * j + 1, cur + 1, tb, lb, std::false_type{});  // past the end: valid 0, all masked
+          if (ta.valid > 0 || tb.valid > 0)
+            attend_pair<D>(st, ta, tb, &lds[cur][LT::KB], &lds[cur + 1][LT::KB], qop, scale_log2, col, grp, la, lb);
+        }
+        wait_vmcnt<0>();  // the next pair landed
+        barrier_lds();    // ... for every wave; every wave is done with this pair
+      }
+    }
+  } else if (n_tiles > 0) {
     issue(0, 0);
     if (n_tiles > 1) {
       issue(1, 1);
