@@ -69,7 +69,8 @@ def pow2_scale(amax: np.ndarray) -> np.ndarray:
 
 def quantize(x: np.ndarray, scale: np.ndarray) -> np.ndarray:
     """``e4m3(clamp(x / scale, -448, 448))`` as attention.py:49 does it (fp32 math)."""
-    v = np.asarray(x, dtype=np.float32) / np.asarray(scale, dtype=np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):  # NaN / inf inputs are part of the domain
+        v = np.asarray(x, dtype=np.float32) / np.asarray(scale, dtype=np.float32)
     v = np.where(np.isnan(v), v, np.clip(v, -E4M3_MAX, E4M3_MAX)).astype(np.float32)
     return e4m3_encode(v)
 
