@@ -128,6 +128,51 @@ __global__ __launch_bounds__(64) void append_fp8_kernel(uint8_t *__restrict__ kc
   fp8_append_one<D, true>(vc, vs, val, vst, vsh, slots, t, r, blk, first, h, H, BS);
 }
 
+// Bulk fp8 append (prompt-sized calls): one wave per (64-token window of the
+// call, KV head). The wave finds the runs that start in its window (a ballot
+// over its 64 slots) and appends each -- K and V, with the same scale rule --
+// with 16-byte loads and K stores; a run that reaches past the window is
+// still this wave's. (One workgroup per token, as the small-call kernel
+// launches, left 15 of 16 idle and each run to dependent 2-byte loads.)
+constexpr int kFp8BulkMinTokens = 64;
+template <int D>
+__global__ __launch_bounds__(64) void append_fp8_bulk_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
+                                                             float *__restrict__ ks, float *__restrict__ vs,
+                                                             const uint16_t *__restrict__ key, int64_t kst,
+                                                             int64_t ksh, const uint16_t *__restrict__ val,
+                                                             int64_t vst, int64_t vsh,
+                                                             const int64_t *__restrict__ slots, int64_t T, int H,
+                                                             int BS, int64_t NB) {
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x;
+  bool start = false;
+  if (t0 + lane < T) {
+    const int64_t slot = slots[t0 + lane];
+    if (slot >= 0 && slot / BS < NB) {
+      const int64_t prev = t0 + lane > 0 ? slots[t0 + lane - 1] : -1;
+      start = !(prev >= 0 && prev / BS == slot / BS);
+    }
+  }
+  unsigned long long starts = __ballot(start);
+  while (starts != 0ull) {  // uniform
+    const int i = __ffsll(static_cast<long long>(starts)) - 1;
+    starts &= starts - 1ull;
+    const int64_t t = t0 + i;
+    const int64_t slot = slots[t];
+    const int64_t blk = slot / BS;
+    int r = 1;
+    while (t + r < T) {
+      const int64_t nx = slots[t + r];
+      if (nx < 0 || nx / BS != blk) break;
+      ++r;
+    }
+    const int first = static_cast<int>(slot % BS);
+    fp8_append_run_vec<D, false>(kc, ks, key, kst, ksh, slots, t, r, blk, first, h, H, BS);
+    fp8_append_run_vec<D, true>(vc, vs, val, vst, vsh, slots, t, r, blk, first, h, H, BS);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Gather: one workgroup per (sequence, block index). Reads follow the
 // physical order (coalesced); writes are 16-byte pieces of the contiguous
@@ -320,7 +365,20 @@ extern "C" int wkv_append_fp8(const wkv_cache_t *cache, const void *key, int64_t
   auto vc = static_cast<uint8_t *>(cache->v);
   auto k = static_cast<const uint16_t *>(key);
   auto v = static_cast<const uint16_t *>(value);
-  if (D == 128)
+  // 16-byte source rows for the bulk kernel's vector loads
+  const bool rows16 = aligned16(key) && aligned16(value) && key_stride_t % 8 == 0 && key_stride_h % 8 == 0 &&
+                      value_stride_t % 8 == 0 && value_stride_h % 8 == 0;
+  if (num_tokens >= kFp8BulkMinTokens && rows16) {
+    const dim3 bgrid(static_cast<unsigned>((num_tokens + 63) / 64), static_cast<unsigned>(H));
+    if (D == 128)
+      append_fp8_bulk_kernel<128><<<bgrid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
+                                                        key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
+                                                        num_tokens, H, cache->block_size, cache->num_blocks);
+    else
+      append_fp8_bulk_kernel<64><<<bgrid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
+                                                       key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
+                                                       num_tokens, H, cache->block_size, cache->num_blocks);
+  } else if (D == 128)
     append_fp8_kernel<128><<<grid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
                                                key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
                                                num_tokens, H, cache->block_size, cache->num_blocks);
