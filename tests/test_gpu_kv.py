@@ -103,6 +103,45 @@ def _exhaustive_bf16_rows(h: int, d: int) -> np.ndarray:
     return bits[order].reshape(-1, h, d)
 
 
+@pytest.mark.parametrize("BS", [16, 32])
+def test_append_fp8_bulk_runs(cuda, BS):
+    """Prompt-sized fp8 appends (the bulk kernel): runs that continue partly filled blocks with
+    growing scales, fresh blocks, runs across 64-token windows, skipped slots between runs,
+    shuffled block order -- bit-exact codes and scales."""
+    NB, H, D = 256, 2, 128
+    rng = np.random.default_rng(BS)
+    kc, vc = paged.empty_cache(NB, BS, H, D, dtype=np.uint8, fill=0xAA)
+    ks = np.zeros((NB, H), np.float32)
+    vs = np.zeros((NB, H), np.float32)
+    cache = PagedKVCache(NB, BS, H, D, kv_dtype="fp8_e4m3", device=cuda)
+    _upload(cache, kc, vc, ks, vs)
+
+    def both(key_bits, val_bits, slots, what):
+        assert len(slots) >= 64  # the bulk kernel's range
+        paged.append_fp8(kc, vc, ks, vs, key_bits, val_bits, slots)
+        cache.append(to_dev_bits(key_bits, BF16, cuda), to_dev_bits(val_bits, BF16, cuda),
+                     torch.from_numpy(np.asarray(slots, np.int64)).to(cuda))
+        _assert_cache_equal(cache, kc, vc, ks, vs, what=what)
+
+    blocks = rng.permutation(NB)[:120]
+    fill = rng.integers(1, BS, 40)
+    s1 = np.concatenate([b * BS + np.arange(f) for b, f in zip(blocks[:40], fill)]).astype(np.int64)
+    both(synth.normal_bf16(synth.stream_key("fp8bulk", BS, "k1"), (len(s1), H, D), std=0.01),
+         synth.normal_bf16(synth.stream_key("fp8bulk", BS, "v1"), (len(s1), H, D), std=0.02), s1, "partial fills")
+    parts = [b * BS + np.arange(f, min(BS, f + int(rng.integers(1, BS)))) for b, f in zip(blocks[:40], fill)]
+    parts += [b * BS + np.arange(int(rng.integers(1, BS + 1))) for b in blocks[40:]]
+    order = rng.permutation(len(parts))
+    s2 = []
+    for i in order:
+        s2.append(parts[i])
+        if rng.random() < 0.3:
+            s2.append(np.full(int(rng.integers(1, 4)), -1))
+    s2 = np.concatenate(s2).astype(np.int64)
+    both(synth.normal_bf16(synth.stream_key("fp8bulk", BS, "k2"), (len(s2), H, D), std=5.0),
+         synth.normal_bf16(synth.stream_key("fp8bulk", BS, "v2"), (len(s2), H, D), std=50.0), s2,
+         "continued and fresh runs")
+
+
 def test_append_fp8_bit_exact_exhaustive_and_scale_growth(cuda):
     NB, BS, H, D = 512, 16, 2, 128
     kc, vc = paged.empty_cache(NB, BS, H, D, dtype=np.uint8, fill=0xAA)
