@@ -43,6 +43,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--layers", type=int, default=0, help="0 = the model's depth (8 rotated layers for MLA)")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--kv-dtype", default="bf16", choices=["bf16", "fp8_e4m3"],
+                    help="KV cache dtype of the qwen3-4b-prefill workload (the decode workloads fix their own)")
     ap.add_argument("--partition", type=int, default=0, help="tokens per split-K partition (0 = library choice)")
     ap.add_argument("--kernel-reps", type=int, default=2, help="passes over all layers for per-launch timing")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle time budget")
@@ -263,6 +265,7 @@ def workload(args, torch, dev) -> dict:
         from wavelet_amd.plan import PrefillStep
 
         n_new, B = 2048, 8
+        kv_dtype = getattr(args, "kv_dtype", "bf16")
         w = synth.make_decode_workload(name, batch=B, num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16,
                                        context_lens=np.full(B, n_new))
         args.layers = args.layers or 36
@@ -271,7 +274,7 @@ def workload(args, torch, dev) -> dict:
         T, HQ, HKV, D, BS = B * n_new, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
         caches, qs, ks, vs, outs = [], [], [], [], []
         for _ in range(args.layers):
-            caches.append(PagedKVCache(w.num_blocks, BS, HKV, D, device=dev))
+            caches.append(PagedKVCache(w.num_blocks, BS, HKV, D, kv_dtype=kv_dtype, device=dev))
             qs.append(torch.randn((T, HQ, D), generator=gen, device=dev).to(torch.bfloat16))
             ks.append(torch.randn((T, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
             vs.append(torch.randn((T, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
@@ -284,13 +287,17 @@ def workload(args, torch, dev) -> dict:
                            max_query_len=n_new, max_seq_len=n_new)
         visible = B * n_new * (n_new + 1) // 2  # (query, key) pairs under the causal mask
         flops = 4 * visible * HQ * D
-        append = T * 2 * HKV * D * (2 + 2) + T * 8
-        attn = T * HQ * D * 2 * 2 + T * 2 * HKV * D * 2  # q in, o out, the prompt's K/V read once
+        fp8 = kv_dtype == "fp8_e4m3"
+        kvb = 1 if fp8 else 2  # cache bytes per element
+        append = T * 2 * HKV * D * (2 + kvb) + T * 8
+        attn = T * HQ * D * 2 * 2 + T * 2 * HKV * D * kvb  # q in, o out, the prompt's K/V read once
         return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
-                "kernel": "prefill_gqa_kernel<128,false> (+ append_bf16_kernel)", "dtype": "bf16",
+                "kernel": ("prefill_gqa_kernel<128,true> (+ append_fp8_bulk_kernel)" if fp8 else
+                           "prefill_gqa_kernel<128,false> (+ append_bf16_kernel)"),
+                "dtype": "bf16" + (" (fp8-e4m3 KV)" if fp8 else ""),
                 "flops_per_layer": flops, "cache_bytes": caches[0].nbytes, "bound": "mfma",
                 "desc": f"Qwen3-4B prompt step: {args.layers} layers x (append + causal prefill attention), "
-                        f"{B} prompts x {n_new} tokens, 32 q / 8 kv heads, d=128, bf16, block 16"}
+                        f"{B} prompts x {n_new} tokens, 32 q / 8 kv heads, d=128, {kv_dtype} KV, block 16"}
     elif name in ("sampler", "sampler-default"):
         # the step after decode: one token per row from bf16 logits over Qwen's vocabulary with
         # processed logprobs and the sampling mask; "sampler": temperature 0.7, top_k 50, top_p 0.9;
