@@ -16,10 +16,12 @@
 // served from that XCD's L2 instead of being fetched by all eight. The
 // latest (most expensive, causally) query tiles are dispatched first.
 // Keys are streamed in 16-token tiles copied once per workgroup into LDS by
-// LDS-DMA (three buffers: two tiles in flight while the waves attend the
-// third with the decode kernels' tile arithmetic, gqa_tiles.h); tiles on the
-// causal diagonal mask per lane (column). Every wave finishes its rows: no
-// split-K, no workspace.
+// LDS-DMA. bf16 caches: four buffers, a pair of tiles attended at once
+// (attend_pair: one row maximum per 32 keys, 16x16x32 PV products) while the
+// next pair is in flight. fp8 caches: three buffers, two tiles in flight while
+// the waves attend the third with the decode kernels' tile arithmetic
+// (gqa_tiles.h). Tiles on the causal diagonal mask per lane (column). Every
+// wave finishes its rows: no split-K, no workspace.
 #include "gqa_tiles.h"
 #include "lds_dma.h"
 
