@@ -13,8 +13,12 @@ Prints one JSON line:
   value        algorithmic bytes of a step / measured step time (GB/s)
   roofline     one layer's fused append + attention launch: algorithmic bytes
                per launch / its mean time (HIP events on the launch stream),
-               against the 8 TB/s HBM peak
-  cpu_baseline the CPU oracle on a bounded sample of the same workload
+               against the 8 TB/s HBM peak; `traffic` is the HBM bytes per
+               launch from the committed rocprofv3 PMC summary named in
+               `traffic_source` (counters cannot be read inside this run)
+  hbm_read_ceiling_gbs  a read-only streaming kernel over 4 GiB, same process
+  cpu_baseline the numpy oracle on a bounded sample of the same workload:
+               median of >= 5 timed repetitions after one warm-up
 """
 
 from __future__ import annotations
@@ -28,6 +32,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+NO_KV_DTYPE = ("deepseek-v3-mla", "sampler", "sampler-default")  # workloads without a GQA KV cache
 MFMA_PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
 
 
@@ -43,8 +48,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--layers", type=int, default=0, help="0 = the model's depth (8 rotated layers for MLA)")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=4096)
-    ap.add_argument("--kv-dtype", default="bf16", choices=["bf16", "fp8_e4m3"],
-                    help="KV cache dtype of the qwen3-4b-prefill workload (the decode workloads fix their own)")
+    ap.add_argument("--kv-dtype", default=None, choices=["bf16", "fp8_e4m3"],
+                    help="KV cache dtype of a GQA workload (default: bf16, fp8_e4m3 for qwen2.5-7b-groups); "
+                         "the MLA and sampler workloads have none")
     ap.add_argument("--partition", type=int, default=0, help="tokens per split-K partition (0 = library choice)")
     ap.add_argument("--kernel-reps", type=int, default=2, help="passes over all layers for per-launch timing")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle time budget")
@@ -70,36 +76,75 @@ def calibrate_copy() -> int:
     return 0
 
 
-def copy_ceiling_gbs(torch, dev, nbytes: int = 1 << 30, buffers: int = 4, reps: int = 8) -> float:
-    """Device-to-device copy rate (read + write bytes / time) over rotating 1 GiB buffers."""
-    src = [torch.empty(nbytes // 4, dtype=torch.float32, device=dev) for _ in range(buffers)]
-    dst = [torch.empty_like(src[0]) for _ in range(buffers)]
-    for t in src:
-        t.fill_(1.0)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for r in range(reps):
-        dst[r % buffers].copy_(src[r % buffers])
-    b.record()
-    torch.cuda.synchronize()
-    gbs = 2 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
-    del src, dst
+def hbm_read_ceiling_gbs(torch, dev, nbytes: int = 4 << 30, reps: int = 5) -> dict:
+    """Best read rate of the library's streaming-read probe over a 4 GiB buffer (16x the
+    256 MB last-level cache), a few grid sizes, HIP events on the launch stream."""
+    from wavelet_amd import _lib
+
+    lib = _lib.load()
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    buf.fill_(0x5A)
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    best, best_blocks = 0.0, 0
+    for blocks in (2048, 4096, 8192, 16384):
+        rc = lib.wkv_hbm_read_probe(buf.data_ptr(), nbytes, blocks, sink.data_ptr(), stream.cuda_stream)
+        _lib.check(rc, "hbm read probe")
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            lib.wkv_hbm_read_probe(buf.data_ptr(), nbytes, blocks, sink.data_ptr(), stream.cuda_stream)
+        b.record(stream)
+        torch.cuda.synchronize()
+        gbs = nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+        if gbs > best:
+            best, best_blocks = gbs, blocks
+    del buf, sink
     torch.cuda.empty_cache()
-    return gbs
+    return {"gbs": round(best, 1), "bytes": nbytes, "workgroups": best_blocks}
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if any."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_gqa_qwen3_4b_pmc.md")
+# committed rocprofv3 PMC summaries per workload (bf16 KV unless named)
+TRAFFIC_PROFILES = {
+    ("qwen3-4b", "bf16"): "profiles/decode_gqa_qwen3_4b_pmc.md",
+    ("qwen3-4b-var", "bf16"): "profiles/decode_gqa_qwen3_4b_var_pmc.md",
+    ("qwen2.5-0.5b", "bf16"): "profiles/decode_gqa_qwen2_5_0_5b_pmc.md",
+}
+
+
+def measured_traffic(workload: str, kv_dtype: str, kernel: str) -> tuple[int | None, str | None]:
+    """HBM bytes per launch of `kernel` from the workload's committed rocprofv3 PMC summary,
+    and where that figure comes from (the summary file and the commit it records), if any."""
+    rel = TRAFFIC_PROFILES.get((workload, kv_dtype))
+    if rel is None:
+        return None, None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), rel)
+    value, commit = None, None
     try:
         with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch") and kernel in line:
-                    return int(line.split()[1])
+                    value = int(line.split()[1])
+                elif line.startswith("source_commit"):
+                    commit = line.split()[1]
+    except OSError:
+        return None, None
+    if value is None:
+        return None, None
+    src = f"{rel}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this workload"
+    return value, src + (f" at commit {commit}" if commit else "")
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    return "unknown"
 
 
 def cpu_baseline(args, hq, hkv, d, bs, scale, per_layer_bytes) -> dict:
@@ -140,24 +185,29 @@ def cpu_baseline(args, hq, hkv, d, bs, scale, per_layer_bytes) -> dict:
                 s /= s.sum(axis=1, keepdims=True)
                 _ = s @ vf[i, :, h]
 
-    one_layer()  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
+    one_layer()  # warm-up, untimed
+    times, t0 = [], time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t0 < args.cpu_seconds and len(times) < 1000):
+        t = time.perf_counter()
         one_layer()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or reps >= 1000:
-            break
+        times.append(time.perf_counter() - t)
     if limiter is not None:
         limiter.unregister() if hasattr(limiter, "unregister") else None
     sample_bytes = per_layer_bytes * nseq / args.batch
+    med = float(np.median(times))
     return {
-        "value": round(sample_bytes * reps / el / 1e9, 3),
+        "value": round(sample_bytes / med / 1e9, 3),
         "unit": "GB/s",
         "cores": int(cores),
         "kind": "port",
-        "sample": f"{reps} x (one layer, {nseq} of the {args.batch} sequences: append 1 token + attention over "
-                  f"{args.context} tokens), {el:.1f} s, numpy oracle",
+        "impl": "numpy restatement of the path (oracle/paged.py: append_bf16, gather, fp32 attention), "
+                "BLAS threads = cores",
+        "cpu_model": cpu_model(),
+        "reps": len(times),
+        "median_s": round(med, 4),
+        "sample": f"median of {len(times)} timed reps after 1 warm-up of (one layer, {nseq} of the {args.batch} "
+                  f"sequences: append 1 token + attention over {args.context} tokens), "
+                  f"{sum(times):.1f} s in total; GB/s = that sample's algorithmic bytes / median time",
     }
 
 
@@ -165,7 +215,6 @@ def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0, grouped
     """Per-layer caches (own memory per layer), step buffers and a DecodeStep plan
     (group-aware when `grouped`: the workload's groups share their prompt blocks)."""
     from wavelet_amd import PagedKVCache
-    from wavelet_amd.plan import DecodeStep
 
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
@@ -190,6 +239,16 @@ def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0, grouped
         ks.append((torch.randn((B, HKV, D), generator=gen, device=dev) * qkv_std).to(torch.bfloat16))
         vs.append((torch.randn((B, HKV, D), generator=gen, device=dev) * qkv_std).to(torch.bfloat16))
         outs.append(torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev))
+    step = gqa_plan(torch, dev, w, caches, qs, ks, vs, outs, args.partition, grouped)
+    return step, caches[0].nbytes
+
+
+def gqa_plan(torch, dev, w, caches, qs, ks, vs, outs, partition: int = 0, grouped: bool = False):
+    """The decode plan every GQA workload times: fused append + attention per layer, the
+    library's partition and dispatch order unless `partition` is given, group-aware when
+    `grouped` (the parity tests build their plans through this same call)."""
+    from wavelet_amd.plan import DecodeStep
+
     bt = torch.from_numpy(w.block_tables).to(dev)
     sl = torch.from_numpy(w.context_lens).to(dev)
     slots = torch.from_numpy(w.new_token_slots()).to(dev)
@@ -198,36 +257,47 @@ def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0, grouped
         n_groups = w.batch // w.group_size
         group = dict(group_size=w.group_size, max_prefix_len=w.prefix_len,
                      prefix_lens=torch.full((n_groups,), w.prefix_len, dtype=torch.int32, device=dev))
-    step = DecodeStep(caches, qs, ks, vs, outs, bt, sl, slots, w.scale, max_seq_len=int(w.context_lens.max()),
-                      partition_size=args.partition, **group)
-    return step, caches[0].nbytes
+    return DecodeStep(caches, qs, ks, vs, outs, bt, sl, slots, w.scale, max_seq_len=int(w.context_lens.max()),
+                      partition_size=partition, **group)
+
+
+def mla_plan(torch, dev, w, caches, q_nope, q_pe, kv_c, k_pe, outs, partition: int = 0):
+    """The MLA decode plan the deepseek-v3-mla workload times (fused latent append + attention)."""
+    from wavelet_amd.plan import MLADecodeStep
+
+    return MLADecodeStep(caches, q_nope, q_pe, kv_c, k_pe, outs, torch.from_numpy(w.block_tables).to(dev),
+                         torch.from_numpy(w.context_lens).to(dev), torch.from_numpy(w.new_token_slots()).to(dev),
+                         w.scale, max_seq_len=int(w.context_lens.max()), partition_size=partition)
 
 
 def workload(args, torch, dev) -> dict:
     """Builds the selected workload: plan, bytes, names (the default is the headline)."""
     from wavelet_amd import MLALatentCache, synth
-    from wavelet_amd.plan import MLADecodeStep
 
     name = args.workload
+    kv_dtype = getattr(args, "kv_dtype", None)
     if name in ("qwen3-4b", "qwen3-4b-var"):
         w = synth.qwen3_4b_workload(batch=args.batch, context=args.context if name == "qwen3-4b" else None)
         args.layers = args.layers or 36
-        step, cache_bytes = _gqa_setup(torch, dev, args, w, "bf16")
-        kv_bytes = 2
-        desc = "Qwen3-4B decode step: 36 layers x (append 1 token/seq + GQA paged decode attention)"
+        kv_dtype = kv_dtype or "bf16"
+        step, cache_bytes = _gqa_setup(torch, dev, args, w, kv_dtype)
+        kv_bytes = 1 if kv_dtype == "fp8_e4m3" else 2
+        desc = f"Qwen3-4B decode step: 36 layers x (append 1 token/seq + GQA paged decode attention), {kv_dtype} KV"
     elif name == "qwen2.5-0.5b":
         w = synth.qwen25_05b_workload()
         args.layers = args.layers or 24
-        step, cache_bytes = _gqa_setup(torch, dev, args, w, "bf16", qkv_std=1 / 8)
-        kv_bytes = 2
-        desc = "Qwen2.5-0.5B decode step: 24 layers x (append + GQA decode), 14 q / 2 kv heads, d=64"
+        kv_dtype = kv_dtype or "bf16"
+        step, cache_bytes = _gqa_setup(torch, dev, args, w, kv_dtype, qkv_std=1 / 8)
+        kv_bytes = 1 if kv_dtype == "fp8_e4m3" else 2
+        desc = f"Qwen2.5-0.5B decode step: 24 layers x (append + GQA decode), 14 q / 2 kv heads, d=64, {kv_dtype} KV"
     elif name == "qwen2.5-7b-groups":
         w = synth.qwen25_7b_group_workload()
         args.layers = args.layers or 28
         grouped = bool(getattr(args, "group_aware", False))
-        step, cache_bytes = _gqa_setup(torch, dev, args, w, "fp8_e4m3", grouped=grouped)
-        kv_bytes = 1
-        desc = ("Qwen2.5-7B GRPO groups, fp8 KV: 28 layers x (fp8 append + GQA decode), 32 x 8 seqs, shared "
+        kv_dtype = kv_dtype or "fp8_e4m3"
+        step, cache_bytes = _gqa_setup(torch, dev, args, w, kv_dtype, grouped=grouped)
+        kv_bytes = 1 if kv_dtype == "fp8_e4m3" else 2
+        desc = (f"Qwen2.5-7B GRPO groups, {kv_dtype} KV: 28 layers x (append + GQA decode), 32 x 8 seqs, shared "
                 "1024-token prompts" + (" (group-aware: each prompt block read once per group)" if grouped else
                                         " (members decoded separately)"))
     elif name == "deepseek-v3-mla":
@@ -246,9 +316,7 @@ def workload(args, torch, dev) -> dict:
             kc.append(torch.randn((B, R), generator=gen, device=dev).to(torch.bfloat16))
             kp.append(torch.randn((B, P), generator=gen, device=dev).to(torch.bfloat16))
             outs.append(torch.empty((B, H, R), dtype=torch.bfloat16, device=dev))
-        step = MLADecodeStep(caches, qn, qp, kc, kp, outs, torch.from_numpy(w.block_tables).to(dev),
-                             torch.from_numpy(w.context_lens).to(dev), torch.from_numpy(w.new_token_slots()).to(dev),
-                             w.scale, max_seq_len=int(w.context_lens.max()), partition_size=args.partition)
+        step = mla_plan(torch, dev, w, caches, qn, qp, kc, kp, outs, args.partition)
         cache_bytes = caches[0].latent.numel() * 2
         L = w.context_lens.astype(np.int64)
         attn = int(L.sum()) * (R + P) * 2 + B * H * (R + P) * 2 + B * H * R * 2 + int(((L + BS - 1) // BS).sum()) * 4 + B * 4
@@ -265,7 +333,7 @@ def workload(args, torch, dev) -> dict:
         from wavelet_amd.plan import PrefillStep
 
         n_new, B = 2048, 8
-        kv_dtype = getattr(args, "kv_dtype", "bf16")
+        kv_dtype = kv_dtype or "bf16"
         w = synth.make_decode_workload(name, batch=B, num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16,
                                        context_lens=np.full(B, n_new))
         args.layers = args.layers or 36
@@ -292,8 +360,10 @@ def workload(args, torch, dev) -> dict:
         append = T * 2 * HKV * D * (2 + kvb) + T * 8
         attn = T * HQ * D * 2 * 2 + T * 2 * HKV * D * kvb  # q in, o out, the prompt's K/V read once
         return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
+                # the append kernel wkv_append(_fp8) picks for T = 16,384 tokens: the bulk paths
+                # from 256 (bf16) / 64 (fp8) tokens on
                 "kernel": ("prefill_gqa_kernel<128,true> (+ append_fp8_bulk_kernel)" if fp8 else
-                           "prefill_gqa_kernel<128,false> (+ append_bf16_kernel)"),
+                           "prefill_gqa_kernel<128,false> (+ append_bf16_bulk_kernel)"),
                 "dtype": "bf16" + (" (fp8-e4m3 KV)" if fp8 else ""),
                 "flops_per_layer": flops, "cache_bytes": caches[0].nbytes, "bound": "mfma",
                 "desc": f"Qwen3-4B prompt step: {args.layers} layers x (append + causal prefill attention), "
@@ -354,11 +424,11 @@ def workload(args, torch, dev) -> dict:
     scales = len(used) * 2 * HKV * 4 if kv_bytes == 1 else 0
     attn = kv_unique + scales + B * HQ * D * 2 * 2 + int(((L + BS - 1) // BS).sum()) * 4 + B * 4
     append = B * 2 * HKV * D * (2 + kv_bytes) + B * 8
+    f8 = "true" if kv_bytes == 1 else "false"
     return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
-            "kernel": (f"decode_gqa_grouped_kernel<{D},true,true,4> (+ decode_grouped_merge_kernel)"
-                       if getattr(step, "grouped", False) else
-                       f"decode_gqa_kernel<{D},{'true' if kv_bytes == 1 else 'false'},true,W>"),
-            "dtype": "fp8_e4m3 KV, bf16 q/o" if kv_bytes == 1 else "bf16", "desc": desc,
+            "kernel": (f"decode_gqa_grouped_kernel<{D},{f8},true,4> (+ merge_partials_kernel)"
+                       if getattr(step, "grouped", False) else f"decode_gqa_kernel<{D},{f8},true,W>"),
+            "dtype": "fp8_e4m3 KV, bf16 q/o" if kv_bytes == 1 else "bf16", "desc": desc, "kv_dtype": kv_dtype,
             "flops_per_layer": 4 * int(L.sum()) * HQ * D, "cache_bytes": cache_bytes,
             "logical_kv_bytes": int(L.sum()) * 2 * HKV * D * kv_bytes}
 
@@ -369,6 +439,9 @@ def main() -> int:
         return calibrate_copy()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); run it with --gpus 1", file=sys.stderr)
+        return 2
+    if args.kv_dtype is not None and args.workload in NO_KV_DTYPE:
+        print(f"--kv-dtype does not apply to the {args.workload} workload", file=sys.stderr)
         return 2
     import torch
 
@@ -415,12 +488,13 @@ def main() -> int:
     split = wl.get("split", True)  # the step has separate append and attention calls
     attend_us = per_launch(step.attend, 1) if split else None
     append_us = per_launch(step.append, 1) if split else None
-    ceiling = copy_ceiling_gbs(torch, dev)
+    ceiling = hbm_read_ceiling_gbs(torch, dev)
 
     step_bytes = wl["layer_bytes"] * args.layers
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = wl["layer_bytes"] / (kernel_us * 1e-6) / 1e9
-    headline = wl["name"] == "qwen3-4b"
+    headline = (wl["name"] == "qwen3-4b" and wl.get("kv_dtype") == "bf16" and w.batch == 64
+                and int(w.context_lens.max()) == 4096 and args.layers == 36)
     B = w.batch
     if wl.get("bound") == "mfma":  # compute-bound workload: TFLOP/s against the dense bf16 MFMA peak
         tflops_step = wl["flops_per_layer"] * args.layers / (ms_per_step * 1e-3) / 1e12
@@ -479,13 +553,21 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(kernel_name) if headline else None,
+            "traffic": None,
             "bytes_per_launch": wl["layer_bytes"],
             "mean_launch_us": round(kernel_us, 2),
             "tflops": round(wl["flops_per_layer"] / (kernel_us * 1e-6) / 1e12, 2),
+            "frac_of_read_ceiling": round(achieved / ceiling["gbs"], 4) if ceiling["gbs"] else None,
         },
-        "hbm_copy_gbs": round(ceiling, 1),
+        "hbm_read_ceiling_gbs": ceiling["gbs"],
+        "hbm_read_ceiling": {"kernel": "hbm_read_probe_kernel (16-byte loads, 8 in flight per lane)",
+                             "bytes": ceiling["bytes"], "workgroups": ceiling["workgroups"]},
     }
+    traffic, source = measured_traffic(wl["name"], wl.get("kv_dtype", ""), kernel_name)
+    if traffic is not None and args.layers == ({"qwen3-4b": 36, "qwen3-4b-var": 36, "qwen2.5-0.5b": 24}
+                                               .get(wl["name"], -1)) and args.partition == 0:
+        rec["roofline"]["traffic"] = traffic
+        rec["roofline"]["traffic_source"] = source
     if split:
         rec["unfused_us"] = {"append": round(append_us, 2), "attention": round(attend_us, 2)}
     if "logical_kv_bytes" in wl and wl["w"].group_size > 1:

@@ -303,6 +303,15 @@ int wkv_append_paged_decode_mla(const wkv_mla_cache_t *cache, const void *kv_c, 
                                 const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
                                 int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* ---- measurement --------------------------------------------------------
+ * Read `bytes` (a multiple of 16) of device memory at `buf` once, with
+ * `blocks` workgroups of 256 threads streaming 16-byte loads, and discard
+ * it: the practical HBM read ceiling a benchmark sets beside a kernel's
+ * achieved bandwidth. sink: `blocks` uint32 of device memory the kernel may
+ * write (it does not, for any data but one 1-in-2^32 checksum). No reference
+ * counterpart: a measuring aid of this library. */
+int wkv_hbm_read_probe(const void *buf, int64_t bytes, int32_t blocks, uint32_t *sink, void *stream);
+
 /* ---- misc ---------------------------------------------------------------- */
 const char *wkv_last_error(void);
 int wkv_version(void);

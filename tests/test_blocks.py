@@ -100,3 +100,34 @@ def test_cached_blocks_are_evicted_lru_when_space_runs_out():
     m.allocate("b", np.arange(100, 164))  # needs all 4: evicts the cached ones
     m.free("b")
     assert m.allocate("c", np.arange(32), cache_salt="s") == 0
+
+
+def test_validate_group_prefix_accepts_true_claims_and_names_false_ones():
+    from wavelet_amd import synth, validate_group_prefix
+
+    w = synth.make_group_workload("vgp", num_groups=3, group_size=4, prefix_len=64,
+                                  gen_lens=np.array([1, 5, 17, 40, 20, 21, 22, 23, 9, 30, 2, 16]), num_kv_heads=1,
+                                  num_q_heads=1, head_dim=64, block_size=16)
+    bt, lens = w.block_tables, w.context_lens
+    ok = np.full(3, 64, np.int32)
+    validate_group_prefix(bt, lens, ok, 4, 16)
+    validate_group_prefix(bt, lens, ok, 4, 16, appending=True)
+    validate_group_prefix(bt, lens, np.array([70, 79, 0], np.int32), 4, 16)  # 70 // 16 = 4 blocks: still shared
+    # a claim reaching into the members' private blocks (group 1's members all hold 84+ tokens)
+    with pytest.raises(ValueError, match="group 1: prefix_lens 80 claims block 4 shared"):
+        validate_group_prefix(bt, lens, np.array([64, 80, 64], np.int32), 4, 16)
+    # a member whose prompt block differs inside a true-looking claim
+    bad = bt.copy()
+    bad[6, 2] = bt[0, 2]
+    with pytest.raises(ValueError, match="member 6 holds block"):
+        validate_group_prefix(bad, lens, ok, 4, 16)
+    validate_group_prefix(bad, lens, np.array([64, 32, 64], np.int32), 4, 16)  # claim stops before block 2
+    # ragged last group (batch 10 in groups of 4) and a claim past every member's length
+    validate_group_prefix(bt[:10], lens[:10], np.array([64, 64, 64], np.int32), 4, 16)
+    short = lens.copy()
+    short[:4] = [65, 65, 65, 65]
+    with pytest.raises(ValueError, match="claims block 4"):
+        validate_group_prefix(bt, lens + 100, np.array([1000, 64, 64], np.int32), 4, 16)
+    validate_group_prefix(bt, short, np.array([1000, 64, 64], np.int32), 4, 16)  # cut to the shortest member
+    with pytest.raises(ValueError, match="one entry per group"):
+        validate_group_prefix(bt, lens, ok[:2], 4, 16)

@@ -299,7 +299,9 @@ def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, 
             pr = np.exp(s - s.max(axis=1, keepdims=True))
             pr /= pr.sum(axis=1, keepdims=True)
             ref[i, h * g:(h + 1) * g] = pr @ vv[:, h]
-    check_attention(paged.bf16_to_f32(bits_of(out)), ref, f"fused {kv_dtype}")
+    # the new tokens are drawn with std 4 (so that mishandling them shows): outputs and their bf16
+    # rounding scale with them
+    check_attention(paged.bf16_to_f32(bits_of(out)), ref, f"fused {kv_dtype}", abs_bound=4 * ATOL)
 
 
 def test_decode_matches_golden_output(cuda, golden_dir):

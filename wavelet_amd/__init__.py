@@ -21,7 +21,7 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
 
 from .attention import decode_order, decode_plan, paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla, prefill_gqa
 from .blocks import BlockManager
-from .cache import MLALatentCache, PagedKVCache, validate_tables
+from .cache import MLALatentCache, PagedKVCache, validate_group_prefix, validate_tables
 from .pool import KVPool
 from .sampler import sample
 
@@ -37,5 +37,6 @@ __all__ = [
     "paged_decode_mla",
     "prefill_gqa",
     "sample",
+    "validate_group_prefix",
     "validate_tables",
 ]

@@ -62,6 +62,7 @@ _SIGNATURES = {
     "wkv_mla_workspace_size": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "wkv_paged_decode_mla": (c_int, [POINTER(WkvMlaCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p]),
     "wkv_append_paged_decode_mla": (c_int, [POINTER(WkvMlaCache), c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p]),
+    "wkv_hbm_read_probe": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
     "wkv_last_error": (c_char_p, []),
     "wkv_version": (c_int, []),
 }

@@ -40,12 +40,18 @@ class _Seq:
 class BlockManager:
     """Allocates physical KV blocks to sequences; one table per sequence."""
 
-    def __init__(self, num_blocks: int, block_size: int, *, enable_prefix_caching: bool = True) -> None:
+    def __init__(self, num_blocks: int, block_size: int, *, enable_prefix_caching: bool = True,
+                 max_model_len: int | None = None) -> None:
         if num_blocks <= 0 or block_size <= 0:
             raise ValueError("num_blocks and block_size must be positive")
+        if max_model_len is not None and int(max_model_len) <= 0:
+            raise ValueError(f"max_model_len must be positive (got {max_model_len})")
         self.num_blocks = int(num_blocks)
         self.block_size = int(block_size)
         self.enable_prefix_caching = enable_prefix_caching
+        # the engine's context limit (RLVLLMConfig.max_model_len, configs/config.py:1005-1009): no sequence
+        # grows past it, and block tables are this many blocks wide
+        self.max_model_len = None if max_model_len is None else int(max_model_len)
         self._free: deque[int] = deque(range(self.num_blocks))
         self._ref = np.zeros(self.num_blocks, dtype=np.int64)
         self._seqs: dict[object, _Seq] = {}
@@ -54,6 +60,13 @@ class BlockManager:
         self._evictable: OrderedDict[int, None] = OrderedDict()  # indexed blocks with ref 0, LRU first
 
     # -- capacity and metrics --------------------------------------------------
+    @property
+    def max_blocks_per_seq(self) -> int | None:
+        """Block-table width that ``max_model_len`` implies (None without a limit)."""
+        if self.max_model_len is None:
+            return None
+        return -(-self.max_model_len // self.block_size)
+
     @property
     def capacity_tokens(self) -> int:
         """``num_gpu_blocks * block_size`` (inference_metrics.py:125-133)."""
@@ -111,6 +124,8 @@ class BlockManager:
         if seq_id in self._seqs:
             raise ValueError(f"sequence {seq_id!r} already allocated")
         tokens = np.asarray(prompt_tokens, dtype=np.int64)
+        if self.max_model_len is not None and len(tokens) > self.max_model_len:
+            raise ValueError(f"prompt of {len(tokens)} tokens is longer than max_model_len {self.max_model_len}")
         bs = self.block_size
         n_full = len(tokens) // bs
         seq = _Seq()
@@ -174,6 +189,10 @@ class BlockManager:
         sequence about to write into a block it still shares gets a private
         copy first.
         """
+        if self.max_model_len is not None:
+            for sid in seq_ids:  # checked before any state changes
+                if self._seqs[sid].length >= self.max_model_len:
+                    raise ValueError(f"sequence {sid!r} is at max_model_len {self.max_model_len}: no further token")
         slots = np.empty(len(seq_ids), dtype=np.int64)
         cow: list[tuple[int, int]] = []
         bs = self.block_size
@@ -238,8 +257,13 @@ class BlockManager:
         return min(shared * self.block_size, min(s.length for s in seqs))
 
     def tables(self, seq_ids, width: int | None = None) -> tuple[np.ndarray, np.ndarray]:
-        """``block_table [B, width]`` int32 (unused entries -1) and ``seq_lens [B]`` int32."""
+        """``block_table [B, width]`` int32 (unused entries -1) and ``seq_lens [B]`` int32.
+
+        ``width`` defaults to ``max_blocks_per_seq`` under a ``max_model_len``
+        (a fixed shape for every step), else to the longest table."""
         seqs = [self._seqs[s] for s in seq_ids]
+        if width is None:
+            width = self.max_blocks_per_seq
         w = max((len(s.blocks) for s in seqs), default=1) if width is None else int(width)
         bt = np.full((len(seqs), max(w, 1)), -1, dtype=np.int32)
         for i, s in enumerate(seqs):

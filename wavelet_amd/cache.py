@@ -289,14 +289,25 @@ class MLALatentCache:
 
 
 def check_tables(block_table: torch.Tensor, seq_lens: torch.Tensor, device: torch.device,
-                 block_size: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Validate ``block_table [B, M] int32`` and ``seq_lens [B] int32`` (device tensors)."""
+                 block_size: int, *, strict: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Validate ``block_table [B, M] int32`` and ``seq_lens [B] int32`` (device tensors).
+
+    A one-shot call may hand in a block table whose rows are not contiguous or
+    a strided ``seq_lens``: those are copied. ``strict`` (the pre-validated
+    plans, which keep the caller's tensors and expect them refilled in place)
+    refuses them instead, since a copy would never see the caller's updates.
+    """
     _require_cuda(block_table, "block_table", device)
     _require_cuda(seq_lens, "seq_lens", device)
     if block_table.dtype != torch.int32 or block_table.dim() != 2:
         raise ValueError(f"block_table must be int32 [B, max_blocks] (got {block_table.dtype} {tuple(block_table.shape)})")
     if seq_lens.dtype != torch.int32 or seq_lens.dim() != 1 or seq_lens.shape[0] != block_table.shape[0]:
         raise ValueError("seq_lens must be int32 [B] matching block_table")
+    if strict:
+        if block_table.stride(1) != 1 or not seq_lens.is_contiguous():
+            raise ValueError("a plan needs a block_table with contiguous rows (stride(1) == 1) and a contiguous "
+                             "seq_lens: it reads the tensors handed to it on every step")
+        return block_table, seq_lens
     if block_table.stride(1) != 1:
         block_table = block_table.contiguous()
     return block_table, seq_lens.contiguous()
@@ -315,3 +326,48 @@ def validate_tables(block_table: torch.Tensor, seq_lens: torch.Tensor, num_block
     ids = block_table[used]
     if ids.numel() and (int(ids.min().item()) < 0 or int(ids.max().item()) >= num_blocks):
         raise ValueError(f"block table references a block outside [0, {num_blocks})")
+
+
+def validate_group_prefix(block_table, seq_lens, prefix_lens, group_size: int, block_size: int, *,
+                          appending: bool = False) -> None:
+    """Debug check (synchronises) of a group-aware decode's ``prefix_lens`` claim.
+
+    ``paged_decode_gqa_grouped`` reads group ``g``'s first ``n_g`` blocks once,
+    through the first member's block table, for every member, where ``n_g =
+    min(prefix_lens[g], shortest member context (minus the token a fused
+    append adds)) // block_size``. It trusts the claim; a member whose table
+    differs inside those blocks would silently attend the first member's
+    blocks. This raises ValueError naming the first such (group, member,
+    block). Accepts torch tensors (any device) or numpy arrays.
+    """
+    import numpy as np
+
+    def host(x):
+        return x.detach().cpu().numpy() if isinstance(x, torch.Tensor) else np.asarray(x)
+
+    bt, lens, pre = host(block_table), host(seq_lens).astype(np.int64), host(prefix_lens).astype(np.int64)
+    group_size = int(group_size)
+    if bt.ndim != 2 or lens.shape != (bt.shape[0],):
+        raise ValueError("block_table must be [B, max_blocks] and seq_lens [B]")
+    batch = bt.shape[0]
+    if group_size < 1:
+        raise ValueError(f"group_size must be positive (got {group_size})")
+    n_groups = -(-batch // group_size)
+    if pre.shape != (n_groups,):
+        raise ValueError(f"prefix_lens must have one entry per group ({n_groups})")
+    if (pre < 0).any():
+        raise ValueError("prefix_lens must be non-negative")
+    for g in range(n_groups):
+        b0, b1 = g * group_size, min((g + 1) * group_size, batch)
+        shortest = int(lens[b0:b1].min()) - (1 if appending else 0)
+        n = max(min(int(pre[g]), shortest), 0) // int(block_size)
+        n = min(n, bt.shape[1])
+        if n == 0:
+            continue
+        lead = bt[b0, :n]
+        for b in range(b0 + 1, b1):
+            diff = np.nonzero(bt[b, :n] != lead)[0]
+            if diff.size:
+                j = int(diff[0])
+                raise ValueError(f"group {g}: prefix_lens {int(pre[g])} claims block {j} shared, but member {b} "
+                                 f"holds block {int(bt[b, j])} where member {b0} holds {int(lead[j])}")

@@ -1,0 +1,49 @@
+// Read-only HBM streaming probe: the ceiling the decode kernels' achieved
+// bandwidth is compared with in the benchmark (the peak 8 TB/s is a
+// datasheet figure; what a kernel can read in practice is measured here, in
+// the same process, on the same buffers' kind of memory).
+//
+// Every lane reads 16-byte pieces, eight loads in flight per iteration, in a
+// grid-stride walk over the buffer; the XOR of everything read decides a
+// store that never happens for real data, so no load can be dropped.
+#include "wkv_common.h"
+
+namespace wkv {
+
+constexpr int kProbeThreads = 256;
+constexpr int kProbeUnroll = 8;
+
+__global__ __launch_bounds__(kProbeThreads) void hbm_read_probe_kernel(const u32x4 *__restrict__ src, int64_t n16,
+                                                                       uint32_t *__restrict__ sink) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kProbeThreads;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + (kProbeUnroll - 1) * stride < n16; i += kProbeUnroll * stride) {
+    u32x4 v[kProbeUnroll];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = src[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  for (; i < n16; i += stride) {
+    const u32x4 v = src[i];
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+}  // namespace wkv
+
+using namespace wkv;
+
+extern "C" int wkv_hbm_read_probe(const void *buf, int64_t bytes, int32_t blocks, uint32_t *sink, void *stream) {
+  WKV_CHECK_ARG(buf != nullptr && aligned16(buf), "buf must be non-NULL and 16-byte aligned");
+  WKV_CHECK_ARG(bytes >= 0 && bytes % 16 == 0, "bytes must be a non-negative multiple of 16");
+  WKV_CHECK_ARG(blocks > 0 && blocks <= (1 << 20), "blocks must be in [1, 2^20]");
+  WKV_CHECK_ARG(sink != nullptr, "sink must hold `blocks` uint32 values");
+  if (bytes == 0) return WKV_OK;
+  hbm_read_probe_kernel<<<blocks, kProbeThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const u32x4 *>(buf), bytes / 16, sink);
+  WKV_CHECK_LAUNCH("hbm read probe");
+  return WKV_OK;
+}

@@ -7,6 +7,11 @@ replays the C-ABI calls directly -- two ctypes calls per layer and no tensor
 inspection -- so host overhead stays far below the GPU time of a step.
 The tensors handed to it must stay alive (and keep their storage) for the
 plan's lifetime; refill them in place between steps.
+
+A plan holds the raw pointers of its caches. ``KVPool.sleep`` /
+``PagedKVCache.sleep`` free that memory and ``wake_up`` allocates new memory,
+so a plan built before a sleep refuses to launch afterwards (RuntimeError):
+build a new plan after ``wake_up``.
 """
 
 from __future__ import annotations
@@ -18,12 +23,40 @@ import torch
 
 from . import _lib
 from .attention import _workspace
-from .cache import PagedKVCache, check_tables
+from .cache import PagedKVCache, _require_cuda, check_tables
 
 
 # Smallest B * Hkv * max_seq_len (token-heads) for which DecodeStep orders
 # its dispatch by default.
 ORDER_MIN_WORK = 1 << 20
+
+
+def _plan_slots(slot_mapping: torch.Tensor, device: torch.device, n: int | None) -> torch.Tensor:
+    """A plan's slot mapping: contiguous int64 on the caches' device, ``n`` entries when given."""
+    _require_cuda(slot_mapping, "slot_mapping", device)
+    if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be a contiguous int64 vector")
+    if n is not None and slot_mapping.numel() != n:
+        raise ValueError(f"slot_mapping must hold one slot per sequence ({n}), got {slot_mapping.numel()}")
+    return slot_mapping
+
+
+class _Live:
+    """The cache descriptors a plan was built on; launching is refused once any
+    cache has been released or re-allocated (sleep / wake_up)."""
+
+    def __init__(self, caches) -> None:
+        self._pairs = [(c, c.descriptor()) for c in caches]
+
+    def check(self, layer: int) -> None:
+        cache, desc = self._pairs[layer]
+        if cache._desc is not desc:
+            state = "asleep" if cache._desc is None else "re-allocated by wake_up"
+            raise RuntimeError(f"layer {layer}: the KV cache this plan was built on is {state}; build a new plan")
+
+    def check_all(self) -> None:
+        for layer in range(len(self._pairs)):
+            self.check(layer)
 
 
 @dataclass
@@ -68,11 +101,12 @@ class DecodeStep:
             raise ValueError("no layers")
         dev = caches[0].device
         c0 = caches[0]
-        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, c0.block_size)
-        if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
-            raise ValueError("slot_mapping must be a contiguous int64 vector")
-        self.slot_mapping = slot_mapping
+        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, c0.block_size, strict=True)
         batch = self.seq_lens.shape[0]
+        self.slot_mapping = slot_mapping = _plan_slots(slot_mapping, dev, batch)
+        if not len(q) == len(key) == len(value) == len(out) == len(caches):
+            raise ValueError("q, key, value and out need one tensor per layer")
+        self._live = _Live(caches)
         lib = _lib.load()
         hq = q[0].shape[1]
         self.grouped = group_size > 0
@@ -128,6 +162,7 @@ class DecodeStep:
 
     def prepare(self) -> None:
         """Compute this step's dispatch order from ``seq_lens`` (one launch)."""
+        self._live.check_all()
         if self.ordered:
             rc = self.lib.wkv_decode_order(self.seq_lens.data_ptr(), self.seq_lens.shape[0], self.order.data_ptr(),
                                            self.stream)
@@ -135,12 +170,14 @@ class DecodeStep:
                 _lib.check(rc, "decode order")
 
     def append(self, layer: int) -> None:
+        self._live.check(layer)
         c = self.calls[layer]
         rc = c.append_fn(*c.append_args)
         if rc:
             _lib.check(rc, f"append layer {layer}")
 
     def attend(self, layer: int) -> None:
+        self._live.check(layer)
         fn = self.lib.wkv_paged_decode_gqa_grouped if self.grouped else self.lib.wkv_paged_decode_gqa
         rc = fn(*self.calls[layer].decode_args)
         if rc:
@@ -148,6 +185,7 @@ class DecodeStep:
 
     def step_layer(self, layer: int) -> None:
         """Append + attention of one layer in a single launch (plus the partition merge)."""
+        self._live.check(layer)
         fn = self.lib.wkv_paged_decode_gqa_grouped if self.grouped else self.lib.wkv_append_paged_decode_gqa
         rc = fn(*self.calls[layer].fused_args)
         if rc:
@@ -171,12 +209,16 @@ class MLADecodeStep:
     def __init__(self, caches, q_nope: list[torch.Tensor], q_pe: list[torch.Tensor], kv_c: list[torch.Tensor],
                  k_pe: list[torch.Tensor], out: list[torch.Tensor], block_table: torch.Tensor, seq_lens: torch.Tensor,
                  slot_mapping: torch.Tensor, scale: float, max_seq_len: int, partition_size: int = 0) -> None:
+        if not caches:
+            raise ValueError("no layers")
         c0 = caches[0]
         dev = c0.device
-        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, c0.block_size)
-        if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
-            raise ValueError("slot_mapping must be a contiguous int64 vector")
+        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, c0.block_size, strict=True)
         batch = self.seq_lens.shape[0]
+        slot_mapping = _plan_slots(slot_mapping, dev, batch)
+        if not len(q_nope) == len(q_pe) == len(kv_c) == len(k_pe) == len(out) == len(caches):
+            raise ValueError("q_nope, q_pe, kv_c, k_pe and out need one tensor per layer")
+        self._live = _Live(caches)
         heads = q_nope[0].shape[1]
         lib = _lib.load()
         need = lib.wkv_mla_workspace_size(batch, heads, c0.kv_lora_rank, max_seq_len, int(partition_size))
@@ -209,17 +251,20 @@ class MLADecodeStep:
         self._keep = (caches, q_nope, q_pe, kv_c, k_pe, out, slot_mapping)
 
     def append(self, layer: int) -> None:
+        self._live.check(layer)
         rc = self.lib.wkv_mla_append(*self.calls[layer][0])
         if rc:
             _lib.check(rc, f"mla append layer {layer}")
 
     def attend(self, layer: int) -> None:
+        self._live.check(layer)
         rc = self.lib.wkv_paged_decode_mla(*self.calls[layer][1])
         if rc:
             _lib.check(rc, f"mla decode layer {layer}")
 
     def step_layer(self, layer: int) -> None:
         """Latent append + attention of one layer in a single launch (plus the partition merge)."""
+        self._live.check(layer)
         rc = self.lib.wkv_append_paged_decode_mla(*self.calls[layer][2])
         if rc:
             _lib.check(rc, f"mla append+decode layer {layer}")
@@ -245,13 +290,17 @@ class PrefillStep:
         if not caches:
             raise ValueError("no layers")
         dev = caches[0].device
-        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, caches[0].block_size)
+        self.block_table, self.seq_lens = check_tables(block_table, seq_lens, dev, caches[0].block_size,
+                                                       strict=True)
         batch = self.seq_lens.shape[0]
+        _require_cuda(cu_seqlens_q, "cu_seqlens_q", dev)
         if (cu_seqlens_q.dtype != torch.int32 or tuple(cu_seqlens_q.shape) != (batch + 1,)
                 or not cu_seqlens_q.is_contiguous() or cu_seqlens_q.device != dev):
             raise ValueError(f"cu_seqlens_q must be a contiguous int32 [{batch + 1}] tensor on {dev}")
-        if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
-            raise ValueError("slot_mapping must be a contiguous int64 vector")
+        slot_mapping = _plan_slots(slot_mapping, dev, None)
+        if not len(q) == len(key) == len(value) == len(out) == len(caches):
+            raise ValueError("q, key, value and out need one tensor per layer")
+        self._live = _Live(caches)
         T = slot_mapping.numel()
         self.lib = lib = _lib.load()
         self.stream = torch.cuda.current_stream(dev).cuda_stream
@@ -277,18 +326,21 @@ class PrefillStep:
         self._keep = (caches, q, key, value, out, cu_seqlens_q, slot_mapping)
 
     def append(self, layer: int) -> None:
+        self._live.check(layer)
         fn, args, _, _ = self.calls[layer]
         rc = fn(*args)
         if rc:
             _lib.check(rc, f"append layer {layer}")
 
     def attend(self, layer: int) -> None:
+        self._live.check(layer)
         rc = self.lib.wkv_prefill_gqa(*self.calls[layer][3])
         if rc:
             _lib.check(rc, f"prefill layer {layer}")
 
     def step_layer(self, layer: int) -> None:
         """Append + causal attention of one layer (two launches: the append, then the attention)."""
+        self._live.check(layer)
         rc = self.lib.wkv_prefill_gqa(*self.calls[layer][2])
         if rc:
             _lib.check(rc, f"append+prefill layer {layer}")
