@@ -191,6 +191,26 @@ int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64
                                 int32_t partition_size, void *workspace, int64_t workspace_bytes,
                                 const int32_t *seq_order, void *stream);
 
+/* Allocation-free variant of wkv_append_paged_decode_gqa, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the same arguments and result
+ * without workspace / workspace_bytes. The split-K partials go to a static
+ * device array of WKV_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends; the call allocates nothing. Geometries needing more scratch than that
+ * (wkv_decode_workspace_size at the launch's partition) fail with
+ * WKV_ERR_INVALID before any launch. The current device must be the one
+ * `stream` belongs to. Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU race. No counterpart in the reference. */
+#define WKV_NOALLOC_SCRATCH_BYTES (32ll << 20)
+
+int wkv_append_paged_decode_gqa_noalloc(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                        int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                        int64_t value_stride_h, const int64_t *slot_mapping, const void *q,
+                                        int64_t q_stride_b, int64_t q_stride_h, void *out, int32_t num_q_heads,
+                                        const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                        const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                                        int32_t partition_size, const int32_t *seq_order, void *stream);
+
 /* Group-aware decode for GRPO groups (the n samples of one prompt):
  * sequences g*group_size .. g*group_size+group_size-1 form group g (the last
  * group may be short), and the first prefix_lens[g] tokens of every member are

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libwkv.so"
 
 WKV_OK, WKV_ERR_INVALID, WKV_ERR_UNSUPPORTED, WKV_ERR_LAUNCH = 0, 1, 2, 3
 WKV_KV_BF16, WKV_KV_FP8_E4M3 = 0, 1
+WKV_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/wkv.h
 
 
 class WkvCache(ctypes.Structure):
@@ -55,6 +56,7 @@ _SIGNATURES = {
     "wkv_decode_plan": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "wkv_paged_decode_gqa": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_void_p]),
     "wkv_append_paged_decode_gqa": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_void_p]),
+    "wkv_append_paged_decode_gqa_noalloc": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_void_p]),
     "wkv_grouped_decode_workspace_size": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "wkv_paged_decode_gqa_grouped": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p]),
     "wkv_prefill_gqa": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_float, c_void_p]),

@@ -11,6 +11,7 @@
 // launch.) The decode-step append can be fused in: the wave that owns a
 // sequence's last partition first writes the new token into the cache, then
 // attends over it.
+#include <atomic>
 #include <cmath>
 
 #include "gqa_tiles.h"
@@ -656,7 +657,8 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
                          int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
                          int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
                          float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
-                         const StepAppend *ap, const int32_t *seq_order, void *stream) {
+                         const StepAppend *ap, const int32_t *seq_order, void *stream,
+                         bool static_scratch = false) {
   int rc = check_cache(cache, -1);
   if (rc) return rc;
   WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
@@ -689,6 +691,11 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   decode_shape(max_seq, partition_size, &W, &max_chunks);
   WKV_CHECK_ARG(max_chunks <= 65535, "too many partitions");
   const int64_t need = wkv_decode_workspace_size(batch, num_q_heads, D, max_seq, partition_size * W);
+  if (max_chunks > 1 && static_scratch)
+    WKV_CHECK_ARG(workspace_bytes >= need,
+                  "this geometry needs %lld bytes of split-K scratch; the allocation-free entry point's static "
+                  "scratch holds %lld (WKV_NOALLOC_SCRATCH_BYTES): use wkv_append_paged_decode_gqa with a workspace",
+                  (long long)need, (long long)workspace_bytes);
   if (max_chunks > 1)
     WKV_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= need,
                   "workspace too small: need %lld bytes, got %lld", (long long)need, (long long)workspace_bytes);
@@ -950,4 +957,65 @@ extern "C" int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void 
   return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
                        max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
                        workspace_bytes, &ap, seq_order, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free fused decode: the split-K partials go to a file-scope device
+// array instead of a caller workspace. Every GPU the library runs on holds its
+// own copy (WKV_NOALLOC_SCRATCH_BYTES) until the process ends. Its address is
+// looked up once per device, with that device current, and kept per device;
+// host code passes that address, never the array's name (in host code the
+// name is only a stand-in for the symbol). Nothing in the scratch has to start
+// at zero: the merge reads only partials that the same call's decode kernel
+// wrote. Calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) uint8_t scratch[WKV_NOALLOC_SCRATCH_BYTES];
+
+namespace wkv {
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void *> g_scratch_ptr[kMaxDevices];
+
+// The scratch address on the calling thread's current device.
+static int noalloc_scratch(void **ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(WKV_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(WKV_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(WKV_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *ptr = p;
+  return WKV_OK;
+}
+
+}  // namespace wkv
+
+extern "C" int wkv_append_paged_decode_gqa_noalloc(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                                   int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                                   int64_t value_stride_h, const int64_t *slot_mapping,
+                                                   const void *q, int64_t q_stride_b, int64_t q_stride_h, void *out,
+                                                   int32_t num_q_heads, const int32_t *block_table,
+                                                   int64_t bt_stride, int32_t max_blocks_per_seq,
+                                                   const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
+                                                   float scale, int32_t partition_size, const int32_t *seq_order,
+                                                   void *stream) {
+  WKV_CHECK_ARG(key && value && aligned16(key) && aligned16(value), "key/value must be non-NULL and 16-byte aligned");
+  WKV_CHECK_ARG(key_stride_t >= 0 && key_stride_h >= 0 && value_stride_t >= 0 && value_stride_h >= 0 &&
+                    (key_stride_t | key_stride_h | value_stride_t | value_stride_h) % 8 == 0,
+                "key/value strides must be non-negative multiples of 8");
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  if (cache != nullptr && cache->kv_dtype == WKV_KV_FP8_E4M3)
+    WKV_CHECK_ARG(cache->k_scale && cache->v_scale, "fp8 cache needs k_scale and v_scale");
+  void *ws = nullptr;
+  const int rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  const StepAppend ap{static_cast<const uint16_t *>(key), key_stride_t, key_stride_h,
+                      static_cast<const uint16_t *>(value), value_stride_t, value_stride_h, slot_mapping};
+  return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
+                       max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, ws,
+                       WKV_NOALLOC_SCRATCH_BYTES, &ap, seq_order, stream, true);
 }
