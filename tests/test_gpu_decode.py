@@ -372,3 +372,54 @@ def test_grpo_group_decode_with_block_manager(cuda, kv_dtype):
             kf, vf = paged.bf16_to_f32(kl), paged.bf16_to_f32(vl)
         ref = paged.decode_gqa(paged.bf16_to_f32(q), kf, vf, bt, lens, scale)
         check_attention(paged.bf16_to_f32(bits_of(out)), ref, f"grpo {kv_dtype} step {step}")
+
+
+@pytest.mark.parametrize("fused,partition", [(False, 0), (True, 0), (False, 1024), (True, 1024)])
+def test_decode_mla_score_spikes_restart_partitions(cuda, fused, partition):
+    """Scores that jump far above a partition's first-step maximum.
+
+    Every head attends the same query here and two latent rows point along it
+    (steps 3 and 20 of the first 1024 tokens, ~90 and ~80 log2-units above
+    everything before them): the online softmax must move its reference twice
+    within one 1024-token partition, or once in each of two partitions with
+    the library's partition (96 tokens here), and the output must still match
+    the float64 oracle."""
+    R, P, H, BS = 512, 64, 128, 64
+    lens = np.array([1500, 4096, 700])
+    w = synth.make_decode_workload(f"mlaspike{int(fused)}{partition}", batch=len(lens), num_kv_heads=1, num_q_heads=H,
+                                   head_dim=R + P, block_size=BS, context_lens=lens, scale=1 / math.sqrt(192.0))
+    own = _owned_mask(w)
+    lat = paged.bf16_to_f32(synth.normal_bf16(synth.stream_key(w.name, "lat"), (w.num_blocks, BS, R + P)))
+    q0 = paged.bf16_to_f32(synth.normal_bf16(synth.stream_key(w.name, "q0"), (R + P,)))
+    unit = q0 / np.linalg.norm(q0)
+    for i in range(w.batch):
+        for pos, mag in ((3 * 32 + 5, 40.0), (20 * 32 + 7, 72.0)):
+            if pos < lens[i] - 1:
+                blk = w.block_tables[i][pos // BS]
+                lat[blk, pos % BS] = unit * mag
+    lat_bits = paged.f32_to_bf16(lat)
+    lat_bits[~own] = NAN16
+    q = np.broadcast_to(q0, (w.batch, H, R + P)).copy()
+    q_bits = paged.f32_to_bf16(q)
+    cache = MLALatentCache(w.num_blocks, BS, R, P, device=cuda)
+    cache.latent.copy_(to_dev_bits(lat_bits, BF16, cuda))
+    dq = to_dev_bits(q_bits, BF16, cuda)
+    bt = torch.from_numpy(w.block_tables).to(cuda)
+    sl = torch.from_numpy(w.context_lens).to(cuda)
+    full = lat_bits.copy()
+    if fused:
+        slots = w.new_token_slots()
+        kv = synth.normal_bf16(synth.stream_key(w.name, "kv"), (w.batch, R + P))
+        full.reshape(-1, R + P)[slots] = kv
+        out = paged_decode_mla(dq[:, :, :R], dq[:, :, R:], cache, bt, sl, w.scale,
+                               new_kv_c=to_dev_bits(np.ascontiguousarray(kv[:, :R]), BF16, cuda),
+                               new_k_pe=to_dev_bits(np.ascontiguousarray(kv[:, R:]), BF16, cuda),
+                               slot_mapping=torch.from_numpy(slots).to(cuda), partition_size=partition)
+    else:
+        out = paged_decode_mla(dq[:, :, :R], dq[:, :, R:], cache, bt, sl, w.scale, partition_size=partition)
+    got = paged.bf16_to_f32(bits_of(out))
+    ref = paged.decode_mla(paged.bf16_to_f32(q_bits), paged.bf16_to_f32(full), w.block_tables, w.context_lens,
+                           w.scale)
+    # the spike rows dominate: outputs are ~72/|q0| * q0 (entries up to ~15), whose bf16 rounding is 2^-9 relative
+    a, r = check_attention(got, ref, f"mla spikes fused={fused} P={partition}", abs_bound=8 * ATOL)
+    print(f"mla spikes fused={fused} P={partition}: err abs {a:.2e} rel {r:.2e}")
