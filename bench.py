@@ -426,7 +426,7 @@ def workload(args, torch, dev) -> dict:
     append = B * 2 * HKV * D * (2 + kv_bytes) + B * 8
     f8 = "true" if kv_bytes == 1 else "false"
     return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
-            "kernel": (f"decode_gqa_grouped_kernel<{D},{f8},true,4> (+ merge_partials_kernel)"
+            "kernel": (f"decode_gqa_grouped_kernel<{D},{f8},true,8> (+ merge_partials_kernel)"
                        if getattr(step, "grouped", False) else f"decode_gqa_kernel<{D},{f8},true,W>"),
             "dtype": "fp8_e4m3 KV, bf16 q/o" if kv_bytes == 1 else "bf16", "desc": desc, "kv_dtype": kv_dtype,
             "flops_per_layer": 4 * int(L.sum()) * HQ * D, "cache_bytes": cache_bytes,

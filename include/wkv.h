@@ -225,7 +225,10 @@ int wkv_append_paged_decode_gqa_noalloc(const wkv_cache_t *cache, const void *ke
  * floating-point reassociation. key, value and slot_mapping are all NULL for
  * attention only. The kernel cuts each group's prefix to whole blocks held by
  * every member (and before a token this call appends); max_prefix_len bounds
- * prefix_lens. workspace: wkv_grouped_decode_workspace_size() bytes. No
+ * prefix_lens. workspace: wkv_grouped_decode_workspace_size() bytes.
+ * seq_order (optional, as for wkv_paged_decode_gqa) dispatches the members'
+ * own tokens longest first; the result does not depend on it (an entry
+ * outside 0..batch-1 leaves that sequence's output unspecified). No
  * reference counterpart computes this (vLLM decodes each member separately);
  * the group semantics are the reference's (engine.py:69-90, :1034-1038). */
 int64_t wkv_grouped_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim,
@@ -239,7 +242,7 @@ int wkv_paged_decode_gqa_grouped(const wkv_cache_t *cache, const void *key, int6
                                  const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
                                  const int32_t *prefix_lens, int32_t group_size, int32_t max_prefix_len,
                                  float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
-                                 void *stream);
+                                 const int32_t *seq_order, void *stream);
 
 /* Varlen GQA prefill / chunked prefill over the paged cache. Sequence b
  * brings n_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] new tokens (rows of q

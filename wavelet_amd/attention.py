@@ -45,6 +45,16 @@ def _query(q: torch.Tensor, name: str, shape: tuple[int, ...], device: torch.dev
     return q
 
 
+def _order(seq_order: torch.Tensor | None, batch: int, dev: torch.device) -> int | None:
+    """The device pointer of a dispatch order (None = batch order), checked."""
+    if seq_order is None:
+        return None
+    if (seq_order.dtype != torch.int32 or tuple(seq_order.shape) != (batch,) or not seq_order.is_contiguous()
+            or seq_order.device != dev):
+        raise ValueError(f"seq_order must be a contiguous int32 [{batch}] tensor on {dev}")
+    return seq_order.data_ptr()
+
+
 def _max_len(seq_lens: torch.Tensor, max_seq_len: int | None) -> int:
     if max_seq_len is not None:
         return int(max_seq_len)
@@ -133,9 +143,6 @@ def paged_decode_gqa(
         out = torch.empty((batch, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, hq, cache.head_dim) or not out.is_contiguous():
         raise ValueError("out must be a contiguous bfloat16 [B, Hq, D] tensor")
-    if seq_order is not None and (seq_order.dtype != torch.int32 or tuple(seq_order.shape) != (batch,)
-                                  or not seq_order.is_contiguous() or seq_order.device != dev):
-        raise ValueError(f"seq_order must be a contiguous int32 [{batch}] tensor on {dev}")
     if batch == 0:
         return out
     lib = _lib.load()
@@ -147,7 +154,7 @@ def paged_decode_gqa(
     tail = (q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq, block_table.data_ptr(),
             block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl, float(scale),
             int(partition_size), ws.data_ptr(), ws.numel(),
-            seq_order.data_ptr() if seq_order is not None else None, _stream(dev))
+            _order(seq_order, batch, dev), _stream(dev))
     if fused:
         rc = lib.wkv_append_paged_decode_gqa(
             ctypes.byref(cache.descriptor()), new_key.data_ptr(), new_key.stride(0), new_key.stride(1),
@@ -174,6 +181,7 @@ def paged_decode_gqa_grouped(
     new_key: torch.Tensor | None = None,
     new_value: torch.Tensor | None = None,
     slot_mapping: torch.Tensor | None = None,
+    seq_order: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``paged_decode_gqa`` for GRPO groups that read their shared prompt once.
 
@@ -184,7 +192,9 @@ def paged_decode_gqa_grouped(
     reassociation); the shared blocks are streamed once per group and KV head
     for all of the group's query rows. Optional fused append as in
     ``paged_decode_gqa`` (the group semantics follow ``SamplingParams(n=...)``,
-    wavelet/inference/engine.py:69-90).
+    wavelet/inference/engine.py:69-90). ``seq_order`` (``decode_order``)
+    dispatches the members' own tokens longest first; the result is the same
+    bit for bit.
     """
     if not isinstance(cache, PagedKVCache):
         raise ValueError("cache must be a PagedKVCache")
@@ -237,7 +247,7 @@ def paged_decode_gqa_grouped(
         ctypes.byref(cache.descriptor()), *head, q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq,
         block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl,
         prefix_lens.data_ptr(), group_size, mpl, float(scale), int(partition_size), ws.data_ptr(), ws.numel(),
-        _stream(dev))
+        _order(seq_order, batch, dev), _stream(dev))
     _lib.check(rc, "paged_decode_gqa_grouped")
     return out
 

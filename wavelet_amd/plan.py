@@ -81,10 +81,11 @@ class DecodeStep:
     groups of ``group_size`` consecutive sequences read their shared prompt
     blocks once per group; ``max_prefix_len`` bounds ``prefix_lens``.
 
-    Otherwise, with ``order_by_length``, ``run`` first computes the step's
-    dispatch order (``decode_order``: longest contexts first, one launch shared
-    by every layer) and each layer's decode dispatches its sequences in that
-    order; the results are the same bit for bit. ``None`` (the default) orders
+    With ``order_by_length``, ``run`` first computes the step's dispatch order
+    (``decode_order``: longest contexts first, one launch shared by every
+    layer) and each layer's decode dispatches its sequences (the group-aware
+    decode: the members' own tokens) in that order; the results are the same
+    bit for bit. ``None`` (the default) orders
     when ``B * Hkv * max_seq_len >= 2**20``: below that a launch is short
     enough (~50 us) that the order's dependent read at each workgroup's start
     costs more than mixed lengths lose. Calling ``step_layer`` / ``attend``
@@ -127,7 +128,7 @@ class DecodeStep:
         self.lib = lib
         if order_by_length is None:
             order_by_length = batch * c0.num_kv_heads * max_seq_len >= ORDER_MIN_WORK
-        self.ordered = bool(order_by_length) and not self.grouped
+        self.ordered = bool(order_by_length)
         # always a permutation of the batch: the identity until prepare() runs
         self.order = torch.arange(batch, dtype=torch.int32, device=dev)
         order_ptr = self.order.data_ptr() if self.ordered else None
@@ -148,7 +149,8 @@ class DecodeStep:
                     self.seq_lens.data_ptr(), batch, int(max_seq_len), ctypes.c_float(scale),
                     int(partition_size), self.workspace.data_ptr(), self.workspace.numel(), self.stream)
             if self.grouped:
-                gtail = (*tail[:11], self.prefix_lens.data_ptr(), int(group_size), int(max_prefix_len), *tail[11:])
+                gtail = (*tail[:11], self.prefix_lens.data_ptr(), int(group_size), int(max_prefix_len), *tail[11:-1],
+                         order_ptr, tail[-1])
                 decode_args = (desc, None, 0, 0, None, 0, 0, None, *gtail)
                 fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
                               vv.stride(1), slot_mapping.data_ptr(), *gtail)
