@@ -329,6 +329,213 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 caches: 32 queries per wave on 32x32x16 MFMAs.
+//
+// Workgroup (32-token query tile, KV head x group of four query heads,
+// sequence), four waves, one query head each; key tiles as above (pairs of
+// 16-token LDS tiles, LDS-DMA, four buffers), now 32 keys x 32 queries per
+// step and wave:
+//   S^T[32 keys, 32 queries] = K Q^T     D/16 MFMAs 32x32x16 (A: 16 bytes of
+//                                        one key row from LDS, B: Q^T held in
+//                                        registers for the whole kernel)
+//   O^T[D, 32 queries] += V^T P^T       2 D/32 MFMAs 32x32x16
+// Lane l holds query l % 32 in both accumulators: 16 scores (key rows
+// 8 (r/4) + 4 (l/32) + r % 4 of S^T) and 16 outputs per 32 d. The PV product
+// takes its 16 keys per step in the order those rows give lane l, so the
+// scores a lane holds after the softmax are exactly its B operand (element e
+// of step s = score r = 8 s + e), and V^T's A operand reads keys
+// 16 s + 4 (l/32) + 0..3 and 16 s + 8 + 4 (l/32) + 0..3 of one d row: two
+// 8-byte LDS reads in the [octet][D][8 tokens] V layout. Per 1,024 scores the
+// softmax is about a hundred VALU instructions (one row maximum across the two
+// lane halves, lazy rescale as in the decode kernels).
+template <int D>
+__global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
+    const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const uint16_t *__restrict__ q, int64_t q_st,
+    int64_t q_sh, uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
+    const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
+    int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
+  using LT = LdsTile<D, false>;
+  constexpr int NBUF = 4;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][LT::BYTES];
+  const int id = blockIdx.x;
+  const int item = (id / (8 * n_qt)) * 8 + (id & 7);
+  const int qt = __builtin_amdgcn_readfirstlane(n_qt - 1 - (id / 8) % n_qt);
+  if (item >= n_items) return;
+  const int b = __builtin_amdgcn_readfirstlane(item / (Hkv * n_hg));
+  const int kvh = __builtin_amdgcn_readfirstlane((item / n_hg) % Hkv);
+  const int hg = item % n_hg;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
+  const int q0 = cu_q[b];
+  const int qlen = cu_q[b + 1] - q0;
+  int L = seq_lens[b];
+  L = L < max_seq ? L : max_seq;
+  const int t0 = qt * 32;
+  if (t0 >= qlen) return;  // the whole workgroup leaves together
+  const int h_local = hg * kPrefillWaves + wave;
+  const bool active = h_local < G;  // an idle wave still copies its share of every tile
+  const int h = kvh * G + (active ? h_local : 0);
+  const int ctx = L - qlen;
+  const int tok = t0 + n;
+  const bool valid = active && tok < qlen;
+  const int pos = ctx + tok;  // query n's position: it sees keys [0, pos]
+
+  // Q^T operand j: lane l holds d = 16 j + 8 (l/32) .. + 7 of query l % 32.
+  bf16x8 qb[D / 16];
+  {
+    const uint16_t *qp = q + static_cast<int64_t>(q0 + (tok < qlen ? tok : t0)) * q_st + static_cast<int64_t>(h) * q_sh;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+      u32x4 w = *reinterpret_cast<const u32x4 *>(qp + 16 * j + 8 * hh);
+      if (!valid) w = u32x4{0u, 0u, 0u, 0u};
+      qb[j] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+  floatx16 o[D / 32];
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[c][r] = 0.f;
+  float m_ref = -INFINITY, l_part = 0.f;
+
+  const int last = (t0 + 32 < qlen ? t0 + 32 : qlen) - 1;
+  const int kend = ctx + last + 1;  // keys [0, kend)
+  const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
+  const int min_pos = ctx + t0;  // the smallest query position of the tile
+  const int region = D * BS * LT::ESZ;
+  const int wave_base = 64 * wave;
+  int okr[NBUF];
+  auto issue = [&](int i, int bi) {
+    const int ts = 16 * i;
+    const int bix = ts / BS;
+    int blk = bix < Mb ? bt[b * bt_stride + bix] : -1;
+    okr[bi] = (blk >= 0 && blk < NB) ? 1 : 0;
+    if (!okr[bi]) blk = 0;
+    const int64_t rbase = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(blk * Hkv + kvh)) * region;
+    const int o0 = ts % BS;
+    const uint32_t dst = lds_addr(&lds[bi][0]);
+#pragma unroll
+    for (int k = 0; k < LT::PER_THREAD; ++k) {
+      const int p0 = 256 * k + wave_base;
+      if (LT::EVEN || p0 < LT::PIECES)
+        copy16_to_lds(tile_piece<D, false>(kc, vc, rbase, o0, BS, p0 + lane),
+                      __builtin_amdgcn_readfirstlane(dst + 16 * p0));
+    }
+  };
+
+  if (n_tiles > 0) {
+    issue(0, 0);
+    if (n_tiles > 1) issue(1, 1);
+    wait_vmcnt<0>();
+    barrier_lds();
+    for (int j = 0; 2 * j < n_tiles; ++j) {
+      const int cur = 2 * (j & 1), nxt = 2 - cur;
+      if (2 * j + 2 < n_tiles) issue(2 * j + 2, nxt);
+      if (2 * j + 3 < n_tiles) issue(2 * j + 3, nxt + 1);
+      const int kb = 32 * j;  // position of the pair's first key
+      // keys of each half the pair holds (0 when the half lies past kend or its block is unmapped)
+      const int va = (okr[cur] && kb < kend) ? (kend - kb < 16 ? kend - kb : 16) : 0;
+      const int vb = (2 * j + 1 < n_tiles && okr[cur + 1]) ? (kend - kb - 16 < 16 ? kend - kb - 16 : 16) : 0;
+      if (active && (va > 0 || vb > 0)) {
+        floatx16 sacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+        const uint8_t *lk = &lds[n < 16 ? cur : cur + 1][0] + (n & 15) * 16;  // key row n of the pair
+#pragma unroll
+        for (int jj = 0; jj < D / 16; ++jj) {
+          const u32x4 a = *reinterpret_cast<const u32x4 *>(lk + (2 * jj + hh) * 256);
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), qb[jj], sacc, 0, 0, 0);
+        }
+        // Score r of this lane: key kb + 8 (r/4) + 4 hh + r % 4.
+        float sv[16];
+        const bool full = va == 16 && vb == 16 && kb + 31 <= min_pos;  // uniform: no mask in this pair
+        if (full) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sv[r] = sacc[r] * scale_log2;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kr = 8 * (r / 4) + 4 * hh + (r % 4);  // key within the pair
+            const bool ok = (kr < 16 ? kr < va : kr - 16 < vb) && kb + kr <= pos;
+            sv[r] = ok ? sacc[r] * scale_log2 : -INFINITY;
+          }
+        }
+        float mt = sv[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sv[r]);
+        {
+          const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+          mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+        }
+        const bool move = mt > m_ref + SOFTMAX_TAU;
+        const float m_new = move ? mt : m_ref;
+        const float corr = (move && m_ref != -INFINITY) ? fast_exp2(m_ref - m_new) : 1.f;
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sv[r] = fast_exp2(sv[r] - m_use);
+          ps += sv[r];
+        }
+        l_part = l_part * corr + ps;
+        m_ref = m_new;
+        if (__any(corr != 1.f)) {
+#pragma unroll
+          for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[c][r] *= corr;
+        }
+        bf16x8 pb[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const u32x4 w = {pack_bf16x2(sv[8 * st], sv[8 * st + 1]), pack_bf16x2(sv[8 * st + 2], sv[8 * st + 3]),
+                           pack_bf16x2(sv[8 * st + 4], sv[8 * st + 5]), pack_bf16x2(sv[8 * st + 6], sv[8 * st + 7])};
+          pb[st] = __builtin_bit_cast(bf16x8, w);
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const int vv = st == 0 ? va : vb;
+          if (vv == 0) continue;  // uniform: a half past the keys or unmapped (its P is zero)
+          const uint8_t *lv = &lds[cur + st][LT::KB] + 8 * hh;
+#pragma unroll
+          for (int c = 0; c < D / 32; ++c) {
+            const int d = 32 * c + n;
+            u32x2 v0 = *reinterpret_cast<const u32x2 *>(lv + d * 16);        // keys 4 hh .. + 3 of the half
+            u32x2 v1 = *reinterpret_cast<const u32x2 *>(lv + (D + d) * 16);  // keys 8 + 4 hh .. + 3
+            if (vv < 16) {  // uniform: slots past the keys may hold NaN
+              v0 = mask_v4(v0, vv, hh);
+              v1 = mask_v4(v1, vv - 8, hh);
+            }
+            const u32x4 w = {v0[0], v0[1], v1[0], v1[1]};
+            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb[st], o[c], 0, 0, 0);
+          }
+        }
+      }
+      wait_vmcnt<0>();  // the next pair landed
+      barrier_lds();    // ... for every wave; every wave is done with this pair
+    }
+  }
+  if (!valid) return;
+  float l = l_part;
+  {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t *op = out + static_cast<int64_t>(q0 + tok) * o_st + static_cast<int64_t>(h) * o_sh;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {  // d = 32 c + 8 g + 4 hh + 0..3
+      u32x2 w;
+      w[0] = f32_to_bf16_bits(o[c][4 * g] * inv) | (f32_to_bf16_bits(o[c][4 * g + 1] * inv) << 16);
+      w[1] = f32_to_bf16_bits(o[c][4 * g + 2] * inv) | (f32_to_bf16_bits(o[c][4 * g + 3] * inv) << 16);
+      *reinterpret_cast<u32x2 *>(op + 32 * c + 8 * g + 4 * hh) = w;
+    }
+  }
+}
+
 }  // namespace wkv
 
 using namespace wkv;
@@ -372,8 +579,10 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   WKV_CHECK_ARG(max_query_len > 0 && max_seq_len >= 0, "max_query_len must be > 0 and max_seq_len >= 0");
   WKV_CHECK_ARG(std::isfinite(scale), "scale must be finite");
   const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
+  const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
   const int n_hg = (G + kPrefillWaves - 1) / kPrefillWaves;
-  const int n_qt = (max_query_len + 15) / 16;
+  const int q_tile = fp8 ? 16 : 32;  // query tokens per workgroup
+  const int n_qt = (max_query_len + q_tile - 1) / q_tile;
   const int64_t n_items = static_cast<int64_t>(batch) * Hkv * n_hg;
   const int64_t n_wg = (n_items + 7) / 8 * 8 * n_qt;
   WKV_CHECK_ARG(n_wg <= INT32_MAX, "prefill grid too large");
@@ -384,17 +593,22 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   auto qq = static_cast<const uint16_t *>(q);
   auto oo = static_cast<uint16_t *>(out);
   const float scale_log2 = scale * 1.4426950408889634f;
-  const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
-#define WKV_PREFILL(Dv, F8)                                                                                       \
-  prefill_gqa_kernel<Dv, F8><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                \
+#define WKV_PREFILL(Dv)                                                                                           \
+  prefill_gqa_kernel<Dv, true><<<grid, 64 * kPrefillWaves, 0, s>>>(                                              \
       kc, vc, cache->k_scale, cache->v_scale, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h,       \
       cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS,           \
       cache->num_blocks, scale_log2, n_qt, static_cast<int>(n_items))
+#define WKV_PREFILL32(Dv)                                                                                         \
+  prefill_gqa32_kernel<Dv><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                  \
+      kc, vc, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h, cu_seqlens_q, seq_lens, block_table,   \
+      bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS, cache->num_blocks, scale_log2, n_qt,             \
+      static_cast<int>(n_items))
   if (D == 128) {
-    if (fp8) WKV_PREFILL(128, true); else WKV_PREFILL(128, false);
+    if (fp8) WKV_PREFILL(128); else WKV_PREFILL32(128);
   } else {
-    if (fp8) WKV_PREFILL(64, true); else WKV_PREFILL(64, false);
+    if (fp8) WKV_PREFILL(64); else WKV_PREFILL32(64);
   }
+#undef WKV_PREFILL32
 #undef WKV_PREFILL
   WKV_CHECK_LAUNCH("paged prefill");
   return WKV_OK;
