@@ -330,26 +330,33 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// bf16 caches: 32 queries per wave on 32x32x16 MFMAs.
+// bf16 caches: QB blocks of 32 queries per wave on 32x32x16 MFMAs.
 //
-// Workgroup (32-token query tile, KV head x group of four query heads,
+// Workgroup (32 QB-token query tile, KV head x group of four query heads,
 // sequence), four waves, one query head each; key tiles as above (pairs of
-// 16-token LDS tiles, LDS-DMA, four buffers), now 32 keys x 32 queries per
-// step and wave:
+// 16-token LDS tiles, LDS-DMA, four buffers), 32 keys per step. Per step and
+// query block:
 //   S^T[32 keys, 32 queries] = K Q^T     D/16 MFMAs 32x32x16 (A: 16 bytes of
 //                                        one key row from LDS, B: Q^T held in
 //                                        registers for the whole kernel)
 //   O^T[D, 32 queries] += V^T P^T       2 D/32 MFMAs 32x32x16
-// Lane l holds query l % 32 in both accumulators: 16 scores (key rows
-// 8 (r/4) + 4 (l/32) + r % 4 of S^T) and 16 outputs per 32 d. The PV product
-// takes its 16 keys per step in the order those rows give lane l, so the
-// scores a lane holds after the softmax are exactly its B operand (element e
-// of step s = score r = 8 s + e), and V^T's A operand reads keys
-// 16 s + 4 (l/32) + 0..3 and 16 s + 8 + 4 (l/32) + 0..3 of one d row: two
-// 8-byte LDS reads in the [octet][D][8 tokens] V layout. Per 1,024 scores the
-// softmax is about a hundred VALU instructions (one row maximum across the two
-// lane halves, lazy rescale as in the decode kernels).
-template <int D>
+// Every K read from LDS feeds the QB blocks' QK products, which form QB
+// independent accumulation chains: with QB = 2 the matrix core has a second
+// chain to work on while a product's result is pending, and the K reads and
+// barriers per MFMA halve. Each block then runs its softmax and PV products
+// (V read per block: P for one block at a time keeps the registers within two
+// waves per SIMD).
+// Lane l holds query l % 32 of each block in both accumulators: 16 scores
+// (rows 8 (r/4) + 4 (l/32) + r % 4 of S^T) and 16 outputs per 32 d. S^T's row
+// i carries key kperm(i) (rows 4..7 and 8..11 of each 16 swapped), so score r
+// of lane l is key 16 (r/8) + 8 (l/32) + r % 8: the scores a lane holds after
+// the softmax are exactly its PV B operand (element e of step s = score
+// 8 s + e), and V^T's A operand -- keys 16 s + 8 (l/32) + 0..7 of one d row --
+// is one 16-byte LDS read in the [octet][D][8 tokens] V layout. The softmax
+// (per 1,024 scores about a hundred VALU instructions: the scale folded into
+// the exponent's FMA, one row maximum across the two lane halves, lazy rescale
+// as in the decode kernels) runs per block.
+template <int D, int QB>
 __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
     const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const uint16_t *__restrict__ q, int64_t q_st,
     int64_t q_sh, uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
@@ -357,6 +364,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
     int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
   using LT = LdsTile<D, false>;
   constexpr int NBUF = 4;
+  constexpr int QT = 32 * QB;  // query tokens per workgroup
   __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][LT::BYTES];
   const int id = blockIdx.x;
   const int item = (id / (8 * n_qt)) * 8 + (id & 7);
@@ -371,58 +379,91 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
   const int qlen = cu_q[b + 1] - q0;
   int L = seq_lens[b];
   L = L < max_seq ? L : max_seq;
-  const int t0 = qt * 32;
+  const int t0 = qt * QT;
   if (t0 >= qlen) return;  // the whole workgroup leaves together
   const int h_local = hg * kPrefillWaves + wave;
   const bool active = h_local < G;  // an idle wave still copies its share of every tile
   const int h = kvh * G + (active ? h_local : 0);
   const int ctx = L - qlen;
-  const int tok = t0 + n;
-  const bool valid = active && tok < qlen;
-  const int pos = ctx + tok;  // query n's position: it sees keys [0, pos]
 
-  // Q^T operand j: lane l holds d = 16 j + 8 (l/32) .. + 7 of query l % 32.
-  bf16x8 qb[D / 16];
-  {
+  // Q^T operand j of block qbi: lane l holds d = 16 j + 8 (l/32) .. + 7 of query 32 qbi + l % 32.
+  bf16x8 qb[QB][D / 16];
+#pragma unroll
+  for (int qbi = 0; qbi < QB; ++qbi) {
+    const int tok = t0 + 32 * qbi + n;
+    const bool valid = active && tok < qlen;
     const uint16_t *qp = q + static_cast<int64_t>(q0 + (tok < qlen ? tok : t0)) * q_st + static_cast<int64_t>(h) * q_sh;
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
       u32x4 w = *reinterpret_cast<const u32x4 *>(qp + 16 * j + 8 * hh);
       if (!valid) w = u32x4{0u, 0u, 0u, 0u};
-      qb[j] = __builtin_bit_cast(bf16x8, w);
+      qb[qbi][j] = __builtin_bit_cast(bf16x8, w);
     }
   }
-  floatx16 o[D / 32];
+  floatx16 o[QB][D / 32];
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c)
+  for (int qbi = 0; qbi < QB; ++qbi)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[c][r] = 0.f;
-  float m_ref = -INFINITY, l_part = 0.f;
+    for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[qbi][c][r] = 0.f;
+  float m_ref[QB], l_part[QB];
+#pragma unroll
+  for (int qbi = 0; qbi < QB; ++qbi) {
+    m_ref[qbi] = -INFINITY;
+    l_part[qbi] = 0.f;
+  }
 
-  const int last = (t0 + 32 < qlen ? t0 + 32 : qlen) - 1;
+  const int last = (t0 + QT < qlen ? t0 + QT : qlen) - 1;
   const int kend = ctx + last + 1;  // keys [0, kend)
   const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
-  const int min_pos = ctx + t0;  // the smallest query position of the tile
   const int region = D * BS * LT::ESZ;
   const int wave_base = 64 * wave;
-  int okr[NBUF];
+  // This lane's piece of copy k of every tile sits at a fixed offset from the
+  // (block, head) region plus the tile's first token; whether the piece is K or
+  // V depends on the wave and k only.
+  uint32_t poff[LT::PER_THREAD];
+#pragma unroll
+  for (int k = 0; k < LT::PER_THREAD; ++k) {
+    const int p = 256 * k + wave_base + lane;
+    if (256 * k + wave_base < LT::KB / 16) {  // K chunk c, token m: ((c BS + m) 16)
+      poff[k] = static_cast<uint32_t>(((p >> 4) * BS + (p & 15)) * 16);
+    } else {  // V row d, octet o: (d BS) 2 + 16 o
+      const int v = p - LT::KB / 16;
+      poff[k] = static_cast<uint32_t>((v % D) * BS * 2 + (v / D) * 16);
+    }
+  }
+  // Block ids of blocks wbase .. wbase + 63 of the sequence, lane i holding
+  // block wbase + i, picked per tile with readlane (no memory access per tile).
+  const int32_t *btrow = bt + b * bt_stride;
+  int wbase = 0;
+  int win = lane < Mb ? btrow[lane] : -1;
+  int okmask = 0;  // bit bi: buffer bi holds a mapped block
   auto issue = [&](int i, int bi) {
     const int ts = 16 * i;
-    const int bix = ts / BS;
-    int blk = bix < Mb ? bt[b * bt_stride + bix] : -1;
-    okr[bi] = (blk >= 0 && blk < NB) ? 1 : 0;
-    if (!okr[bi]) blk = 0;
-    const int64_t rbase = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(blk * Hkv + kvh)) * region;
-    const int o0 = ts % BS;
+    const int bix = ts / BS;  // BS is a multiple of 16: one block per tile
+    if (bix >= wbase + 64) {  // uniform: the next 64 blocks (once per 64 blocks; its wait drains the copies)
+      wbase += 64;
+      win = wbase + lane < Mb ? btrow[wbase + lane] : -1;
+    }
+    int blk = __builtin_amdgcn_readlane(win, bix - wbase);
+    const bool ok = blk >= 0 && blk < NB;
+    okmask = ok ? (okmask | (1 << bi)) : (okmask & ~(1 << bi));
+    if (!ok) blk = 0;
+    const int64_t rbase = static_cast<int64_t>(blk * Hkv + kvh) * region;
+    const int o0 = ts - bix * BS;
+    const uint8_t *kbase = kc + rbase + o0 * 16;
+    const uint8_t *vbase = vc + rbase + o0 * 2;
     const uint32_t dst = lds_addr(&lds[bi][0]);
 #pragma unroll
     for (int k = 0; k < LT::PER_THREAD; ++k) {
-      const int p0 = 256 * k + wave_base;
+      const int p0 = 256 * k + wave_base;  // uniform
       if (LT::EVEN || p0 < LT::PIECES)
-        copy16_to_lds(tile_piece<D, false>(kc, vc, rbase, o0, BS, p0 + lane),
-                      __builtin_amdgcn_readfirstlane(dst + 16 * p0));
+        copy16_to_lds((p0 < LT::KB / 16 ? kbase : vbase) + poff[k], __builtin_amdgcn_readfirstlane(dst + 16 * p0));
     }
   };
+  // A row n of S^T carries key kperm(n) of the pair.
+  const int kn = (n & 16) | (((n >> 2) & 3) == 1 ? (n & 3) + 8 : ((n >> 2) & 3) == 2 ? (n & 3) + 4 : (n & 15));
 
   if (n_tiles > 0) {
     issue(0, 0);
@@ -435,80 +476,84 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
       if (2 * j + 3 < n_tiles) issue(2 * j + 3, nxt + 1);
       const int kb = 32 * j;  // position of the pair's first key
       // keys of each half the pair holds (0 when the half lies past kend or its block is unmapped)
-      const int va = (okr[cur] && kb < kend) ? (kend - kb < 16 ? kend - kb : 16) : 0;
-      const int vb = (2 * j + 1 < n_tiles && okr[cur + 1]) ? (kend - kb - 16 < 16 ? kend - kb - 16 : 16) : 0;
+      const int va = (((okmask >> cur) & 1) && kb < kend) ? (kend - kb < 16 ? kend - kb : 16) : 0;
+      const int vb =
+          (2 * j + 1 < n_tiles && ((okmask >> (cur + 1)) & 1)) ? (kend - kb - 16 < 16 ? kend - kb - 16 : 16) : 0;
       if (active && (va > 0 || vb > 0)) {
-        floatx16 sacc;
+        floatx16 sacc[QB];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
-        const uint8_t *lk = &lds[n < 16 ? cur : cur + 1][0] + (n & 15) * 16;  // key row n of the pair
+        for (int qbi = 0; qbi < QB; ++qbi)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[qbi][r] = 0.f;
+        const uint8_t *lk = &lds[kn < 16 ? cur : cur + 1][0] + (kn & 15) * 16;
 #pragma unroll
         for (int jj = 0; jj < D / 16; ++jj) {
-          const u32x4 a = *reinterpret_cast<const u32x4 *>(lk + (2 * jj + hh) * 256);
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), qb[jj], sacc, 0, 0, 0);
-        }
-        // Score r of this lane: key kb + 8 (r/4) + 4 hh + r % 4.
-        float sv[16];
-        const bool full = va == 16 && vb == 16 && kb + 31 <= min_pos;  // uniform: no mask in this pair
-        if (full) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + (2 * jj + hh) * 256));
 #pragma unroll
-          for (int r = 0; r < 16; ++r) sv[r] = sacc[r] * scale_log2;
-        } else {
+          for (int qbi = 0; qbi < QB; ++qbi)
+            sacc[qbi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[qbi][jj], sacc[qbi], 0, 0, 0);
+        }
+        // Per block: softmax, then its PV products (its P never waits in registers
+        // for the other block's softmax).
+#pragma unroll
+        for (int qbi = 0; qbi < QB; ++qbi) {
+          // Score r of this lane (raw, unscaled): key kb + 16 (r/8) + 8 hh + r % 8;
+          // the softmax works on the accumulator in place.
+          floatx16 &sv = sacc[qbi];
+          const int min_pos = ctx + t0 + 32 * qbi;  // the block's smallest query position
+          if (!(va == 16 && vb == 16 && kb + 31 <= min_pos)) {  // uniform: masks in this pair
+            const int pos = min_pos + n;  // this lane's query sees keys [0, pos]
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kr = 16 * (r / 8) + 8 * hh + (r % 8);  // key within the pair
+              const bool ok = (kr < 16 ? kr < va : kr - 16 < vb) && kb + kr <= pos;
+              if (!ok) sv[r] = -INFINITY;
+            }
+          }
+          float mt = sv[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sv[r]);
+          {
+            const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1])) * scale_log2;  // the scale is positive
+          }
+          const bool move = mt > m_ref[qbi] + SOFTMAX_TAU;
+          const float m_new = move ? mt : m_ref[qbi];
+          const float corr = (move && m_ref[qbi] != -INFINITY) ? fast_exp2(m_ref[qbi] - m_new) : 1.f;
+          const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+          float ps = 0.f;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int kr = 8 * (r / 4) + 4 * hh + (r % 4);  // key within the pair
-            const bool ok = (kr < 16 ? kr < va : kr - 16 < vb) && kb + kr <= pos;
-            sv[r] = ok ? sacc[r] * scale_log2 : -INFINITY;
+            sv[r] = fast_exp2(__builtin_fmaf(sv[r], scale_log2, -m_use));  // masked: -inf -> 0
+            ps += sv[r];
           }
-        }
-        float mt = sv[0];
+          l_part[qbi] = l_part[qbi] * corr + ps;
+          m_ref[qbi] = m_new;
+          if (__any(corr != 1.f)) {
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sv[r]);
-        {
-          const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-          mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
-        }
-        const bool move = mt > m_ref + SOFTMAX_TAU;
-        const float m_new = move ? mt : m_ref;
-        const float corr = (move && m_ref != -INFINITY) ? fast_exp2(m_ref - m_new) : 1.f;
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        float ps = 0.f;
+            for (int c = 0; c < D / 32; ++c)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sv[r] = fast_exp2(sv[r] - m_use);
-          ps += sv[r];
-        }
-        l_part = l_part * corr + ps;
-        m_ref = m_new;
-        if (__any(corr != 1.f)) {
+              for (int r = 0; r < 16; ++r) o[qbi][c][r] *= corr;
+          }
 #pragma unroll
-          for (int c = 0; c < D / 32; ++c)
+          for (int st = 0; st < 2; ++st) {
+            const int vv = st == 0 ? va : vb;
+            if (vv == 0) continue;  // uniform: a half past the keys or unmapped (its P is zero)
+            const u32x4 pw = {pack_bf16x2(sv[8 * st], sv[8 * st + 1]), pack_bf16x2(sv[8 * st + 2], sv[8 * st + 3]),
+                              pack_bf16x2(sv[8 * st + 4], sv[8 * st + 5]),
+                              pack_bf16x2(sv[8 * st + 6], sv[8 * st + 7])};
+            const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+            const uint8_t *lv = &lds[cur + st][LT::KB] + hh * D * 16;  // octet hh: keys 8 hh .. 8 hh + 7
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[c][r] *= corr;
-        }
-        bf16x8 pb[2];
+            for (int c = 0; c < D / 32; ++c) {
+              u32x4 w = *reinterpret_cast<const u32x4 *>(lv + (32 * c + n) * 16);
+              if (vv < 16) {  // uniform: slots past the keys may hold NaN
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const u32x4 w = {pack_bf16x2(sv[8 * st], sv[8 * st + 1]), pack_bf16x2(sv[8 * st + 2], sv[8 * st + 3]),
-                           pack_bf16x2(sv[8 * st + 4], sv[8 * st + 5]), pack_bf16x2(sv[8 * st + 6], sv[8 * st + 7])};
-          pb[st] = __builtin_bit_cast(bf16x8, w);
-        }
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const int vv = st == 0 ? va : vb;
-          if (vv == 0) continue;  // uniform: a half past the keys or unmapped (its P is zero)
-          const uint8_t *lv = &lds[cur + st][LT::KB] + 8 * hh;
-#pragma unroll
-          for (int c = 0; c < D / 32; ++c) {
-            const int d = 32 * c + n;
-            u32x2 v0 = *reinterpret_cast<const u32x2 *>(lv + d * 16);        // keys 4 hh .. + 3 of the half
-            u32x2 v1 = *reinterpret_cast<const u32x2 *>(lv + (D + d) * 16);  // keys 8 + 4 hh .. + 3
-            if (vv < 16) {  // uniform: slots past the keys may hold NaN
-              v0 = mask_v4(v0, vv, hh);
-              v1 = mask_v4(v1, vv - 8, hh);
+                for (int e = 0; e < 8; ++e)
+                  if (8 * hh + e >= vv) w[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+              }
+              o[qbi][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb, o[qbi][c], 0, 0, 0);
             }
-            const u32x4 w = {v0[0], v0[1], v1[0], v1[1]};
-            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb[st], o[c], 0, 0, 0);
           }
         }
       }
@@ -516,24 +561,37 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
       barrier_lds();    // ... for every wave; every wave is done with this pair
     }
   }
-  if (!valid) return;
-  float l = l_part;
-  {
-    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
-    l = __uint_as_float(x[0]) + __uint_as_float(x[1]);
-  }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t *op = out + static_cast<int64_t>(q0 + tok) * o_st + static_cast<int64_t>(h) * o_sh;
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) {
+  for (int qbi = 0; qbi < QB; ++qbi) {
+    const int tok = t0 + 32 * qbi + n;
+    if (!active || tok >= qlen) continue;
+    float l = l_part[qbi];
+    {
+      const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+      l = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t *op = out + static_cast<int64_t>(q0 + tok) * o_st + static_cast<int64_t>(h) * o_sh;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {  // d = 32 c + 8 g + 4 hh + 0..3
-      u32x2 w;
-      w[0] = f32_to_bf16_bits(o[c][4 * g] * inv) | (f32_to_bf16_bits(o[c][4 * g + 1] * inv) << 16);
-      w[1] = f32_to_bf16_bits(o[c][4 * g + 2] * inv) | (f32_to_bf16_bits(o[c][4 * g + 3] * inv) << 16);
-      *reinterpret_cast<u32x2 *>(op + 32 * c + 8 * g + 4 * hh) = w;
+    for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {  // d = 32 c + 8 g + 4 hh + 0..3
+        const u32x2 w = {pack_bf16x2(o[qbi][c][4 * g] * inv, o[qbi][c][4 * g + 1] * inv),
+                         pack_bf16x2(o[qbi][c][4 * g + 2] * inv, o[qbi][c][4 * g + 3] * inv)};
+        *reinterpret_cast<u32x2 *>(op + 32 * c + 8 * g + 4 * hh) = w;
+      }
     }
   }
+}
+
+// Query blocks of 32 per wave of the bf16 prefill. One: at d=128 two blocks
+// need 256 VGPRs (two waves per SIMD, with spills) and measured 540 against
+// 420 us per layer for one block at three waves per SIMD on 8 x 2,048-token
+// Qwen3-4B prompts -- the waves that hide each other's latency matter more
+// than a second MFMA chain per wave.
+template <int D>
+constexpr int prefill_query_blocks() {
+  return 1;
 }
 
 }  // namespace wkv
@@ -581,7 +639,7 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
   const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
   const int n_hg = (G + kPrefillWaves - 1) / kPrefillWaves;
-  const int q_tile = fp8 ? 16 : 32;  // query tokens per workgroup
+  const int q_tile = fp8 ? 16 : 32 * (D == 128 ? prefill_query_blocks<128>() : prefill_query_blocks<64>());
   const int n_qt = (max_query_len + q_tile - 1) / q_tile;
   const int64_t n_items = static_cast<int64_t>(batch) * Hkv * n_hg;
   const int64_t n_wg = (n_items + 7) / 8 * 8 * n_qt;
@@ -599,7 +657,7 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
       cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS,           \
       cache->num_blocks, scale_log2, n_qt, static_cast<int>(n_items))
 #define WKV_PREFILL32(Dv)                                                                                         \
-  prefill_gqa32_kernel<Dv><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                  \
+  prefill_gqa32_kernel<Dv, prefill_query_blocks<Dv>()><<<grid, 64 * kPrefillWaves, 0, s>>>(                     \
       kc, vc, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h, cu_seqlens_q, seq_lens, block_table,   \
       bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS, cache->num_blocks, scale_log2, n_qt,             \
       static_cast<int>(n_items))
