@@ -31,6 +31,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// p[min(idx, n - 1)] for idx < n, else -1 (n >= 1), loaded and waited for in
+// one asm block: the compiler's wait-count insertion never sees a load whose
+// result it would guard with a vmcnt(0) at every later use, a wait that would
+// also drain the LDS-DMA copies in flight. The wait here drains them too, so
+// a kernel calls this rarely.
+__device__ __forceinline__ int load_i32_drained(const int32_t *p, int idx, int n) {
+  const int32_t *a = p + (idx < n ? idx : n - 1);
+  int v;
+  asm volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+  return idx < n ? v : -1;
+}
+
 // Workgroup barrier for LDS: this wave's LDS accesses complete, then s_barrier.
 __device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 

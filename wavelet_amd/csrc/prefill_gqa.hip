@@ -422,58 +422,71 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
   // This lane's piece of copy k of every tile sits at a fixed offset from the
   // (block, head) region plus the tile's first token; whether the piece is K or
   // V depends on the wave and k only.
-  uint32_t poff[LT::PER_THREAD];
+  // pbase[k]: the cache (K or V) plus this lane's offset; the tile's first
+  // token o0 adds o0 << oshift[k] (16-byte K rows, 2-byte V elements).
+  const uint8_t *pbase[LT::PER_THREAD];
+  int oshift[LT::PER_THREAD];
 #pragma unroll
   for (int k = 0; k < LT::PER_THREAD; ++k) {
     const int p = 256 * k + wave_base + lane;
     if (256 * k + wave_base < LT::KB / 16) {  // K chunk c, token m: ((c BS + m) 16)
-      poff[k] = static_cast<uint32_t>(((p >> 4) * BS + (p & 15)) * 16);
+      pbase[k] = kc + ((p >> 4) * BS + (p & 15)) * 16;
+      oshift[k] = 4;
     } else {  // V row d, octet o: (d BS) 2 + 16 o
       const int v = p - LT::KB / 16;
-      poff[k] = static_cast<uint32_t>((v % D) * BS * 2 + (v / D) * 16);
+      pbase[k] = vc + (v % D) * BS * 2 + (v / D) * 16;
+      oshift[k] = 1;
     }
   }
   // Block ids of blocks wbase .. wbase + 63 of the sequence, lane i holding
   // block wbase + i, picked per tile with readlane (no memory access per tile).
   const int32_t *btrow = bt + b * bt_stride;
   int wbase = 0;
-  int win = lane < Mb ? btrow[lane] : -1;
+  int win = load_i32_drained(btrow, lane, Mb);
   int okmask = 0;  // bit bi: buffer bi holds a mapped block
-  auto issue = [&](int i, int bi) {
-    const int ts = 16 * i;
-    const int bix = ts / BS;  // BS is a multiple of 16: one block per tile
-    if (bix >= wbase + 64) {  // uniform: the next 64 blocks (once per 64 blocks; its wait drains the copies)
-      wbase += 64;
-      win = wbase + lane < Mb ? btrow[wbase + lane] : -1;
+  // Tiles are issued in order 0, 1, 2, ...: the next one's block (within the
+  // window) and first token in it advance by 16 tokens per call (BS is a
+  // multiple of 16: one block per tile), with no division.
+  int nbix = 0, no0 = 0;
+  auto issue = [&](int bi) {
+    const int o0 = no0;
+    int bix = nbix;
+    no0 += 16;
+    if (no0 == BS) {
+      no0 = 0;
+      ++nbix;
     }
-    int blk = __builtin_amdgcn_readlane(win, bix - wbase);
+    if (bix == 64) {  // uniform: the next 64 blocks (once per 64 blocks; its wait drains the copies)
+      wbase += 64;
+      nbix -= 64;
+      bix = 0;
+      win = load_i32_drained(btrow, wbase + lane, Mb);
+    }
+    int blk = __builtin_amdgcn_readlane(win, bix);
     const bool ok = blk >= 0 && blk < NB;
     okmask = ok ? (okmask | (1 << bi)) : (okmask & ~(1 << bi));
     if (!ok) blk = 0;
     const int64_t rbase = static_cast<int64_t>(blk * Hkv + kvh) * region;
-    const int o0 = ts - bix * BS;
-    const uint8_t *kbase = kc + rbase + o0 * 16;
-    const uint8_t *vbase = vc + rbase + o0 * 2;
     const uint32_t dst = lds_addr(&lds[bi][0]);
 #pragma unroll
     for (int k = 0; k < LT::PER_THREAD; ++k) {
       const int p0 = 256 * k + wave_base;  // uniform
       if (LT::EVEN || p0 < LT::PIECES)
-        copy16_to_lds((p0 < LT::KB / 16 ? kbase : vbase) + poff[k], __builtin_amdgcn_readfirstlane(dst + 16 * p0));
+        copy16_to_lds(pbase[k] + (rbase + (o0 << oshift[k])), __builtin_amdgcn_readfirstlane(dst + 16 * p0));
     }
   };
   // A row n of S^T carries key kperm(n) of the pair.
   const int kn = (n & 16) | (((n >> 2) & 3) == 1 ? (n & 3) + 8 : ((n >> 2) & 3) == 2 ? (n & 3) + 4 : (n & 15));
 
   if (n_tiles > 0) {
-    issue(0, 0);
-    if (n_tiles > 1) issue(1, 1);
+    issue(0);
+    if (n_tiles > 1) issue(1);
     wait_vmcnt<0>();
     barrier_lds();
     for (int j = 0; 2 * j < n_tiles; ++j) {
       const int cur = 2 * (j & 1), nxt = 2 - cur;
-      if (2 * j + 2 < n_tiles) issue(2 * j + 2, nxt);
-      if (2 * j + 3 < n_tiles) issue(2 * j + 3, nxt + 1);
+      if (2 * j + 2 < n_tiles) issue(nxt);
+      if (2 * j + 3 < n_tiles) issue(nxt + 1);
       const int kb = 32 * j;  // position of the pair's first key
       // keys of each half the pair holds (0 when the half lies past kend or its block is unmapped)
       const int va = (((okmask >> cur) & 1) && kb < kend) ? (kend - kb < 16 ? kend - kb : 16) : 0;
