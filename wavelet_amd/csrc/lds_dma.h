@@ -22,6 +22,15 @@ namespace wkv {
 __device__ __forceinline__ void copy16_to_lds(const void *g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
 }
+// The same copy through a buffer resource: 16 bytes at voff + soff of the
+// resource's base (voff per lane, soff uniform: one SGPR offset per copy
+// instead of a 64-bit address add per lane).
+__device__ __forceinline__ void buffer_copy16_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                                     uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r),
+               "s"(soff)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Waits until at most N of this wave's vector-memory operations are pending.

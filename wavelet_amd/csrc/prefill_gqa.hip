@@ -330,12 +330,31 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Pair slots of the bf16 prefill's LDS ring: pairs of 16-token tiles in
+// flight = slots - 1.
+constexpr int kPrefillPairSlots = 2;
+
+// Waits until at most min(t, T) tiles' copies (PT per tile) of this wave are
+// pending (t uniform).
+template <int PT, int T>
+__device__ __forceinline__ void wait_tiles_pending(int t) {
+  if constexpr (T > 0) {
+    if (t >= T) {
+      wait_vmcnt<T * PT>();
+      return;
+    }
+    wait_tiles_pending<PT, T - 1>(t);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
 // bf16 caches: QB blocks of 32 queries per wave on 32x32x16 MFMAs.
 //
 // Workgroup (32 QB-token query tile, KV head x group of four query heads,
 // sequence), four waves, one query head each; key tiles as above (pairs of
-// 16-token LDS tiles, LDS-DMA, four buffers), 32 keys per step. Per step and
-// query block:
+// 16-token LDS tiles, LDS-DMA, a ring of kPrefillPairSlots pairs), 32 keys per
+// step. Per step and query block:
 //   S^T[32 keys, 32 queries] = K Q^T     D/16 MFMAs 32x32x16 (A: 16 bytes of
 //                                        one key row from LDS, B: Q^T held in
 //                                        registers for the whole kernel)
@@ -363,7 +382,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
     const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
     int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
   using LT = LdsTile<D, false>;
-  constexpr int NBUF = 4;
+  static_assert(LT::EVEN, "every wave issues PER_THREAD copies per tile (the waits count on it)");
+  constexpr int NPAIR = kPrefillPairSlots;
+  constexpr int NBUF = 2 * NPAIR;
   constexpr int QT = 32 * QB;  // query tokens per workgroup
   __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][LT::BYTES];
   const int id = blockIdx.x;
@@ -479,14 +500,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
   const int kn = (n & 16) | (((n >> 2) & 3) == 1 ? (n & 3) + 8 : ((n >> 2) & 3) == 2 ? (n & 3) + 4 : (n & 15));
 
   if (n_tiles > 0) {
-    issue(0);
-    if (n_tiles > 1) issue(1);
-    wait_vmcnt<0>();
+    // Pair p sits in buffers 2 (p mod NPAIR), +1. Pairs 0 .. NPAIR - 2 go out
+    // first; step j issues pair j + NPAIR - 1 into the slot pair j - 1 left
+    // (every wave was done with it at the last barrier), so a pair's copies
+    // have NPAIR - 1 steps to land.
+    for (int t = 0; t < 2 * (NPAIR - 1) && t < n_tiles; ++t) issue(t);
+    wait_tiles_pending<LT::PER_THREAD, 2 * (NPAIR - 2)>((n_tiles < 2 * (NPAIR - 1) ? n_tiles : 2 * (NPAIR - 1)) -
+                                                        (n_tiles < 2 ? n_tiles : 2));  // pair 0 landed
     barrier_lds();
+    int cur = 0;  // buffer of pair j's first tile
     for (int j = 0; 2 * j < n_tiles; ++j) {
-      const int cur = 2 * (j & 1), nxt = 2 - cur;
-      if (2 * j + 2 < n_tiles) issue(nxt);
-      if (2 * j + 3 < n_tiles) issue(nxt + 1);
+      const int nxt = cur == 0 ? NBUF - 2 : cur - 2;
+      const int ti = 2 * (j + NPAIR - 1);
+      if (ti < n_tiles) issue(nxt);
+      if (ti + 1 < n_tiles) issue(nxt + 1);
       const int kb = 32 * j;  // position of the pair's first key
       // keys of each half the pair holds (0 when the half lies past kend or its block is unmapped)
       const int va = (((okmask >> cur) & 1) && kb < kend) ? (kend - kb < 16 ? kend - kb : 16) : 0;
@@ -570,8 +597,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
           }
         }
       }
-      wait_vmcnt<0>();  // the next pair landed
-      barrier_lds();    // ... for every wave; every wave is done with this pair
+      {
+        // pair j + 1 landed (the tiles of pairs j + 2 .. j + NPAIR - 1 may be in flight) ...
+        const int after = n_tiles - 2 * (j + 2);
+        wait_tiles_pending<LT::PER_THREAD, 2 * (NPAIR - 2)>(after < 0 ? 0 : after);
+      }
+      barrier_lds();  // ... for every wave; every wave is done with pair j
+      cur = cur == NBUF - 2 ? 0 : cur + 2;
     }
   }
 #pragma unroll
@@ -593,6 +625,279 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa32_kernel(
                          pack_bf16x2(o[qbi][c][4 * g + 2] * inv, o[qbi][c][4 * g + 3] * inv)};
         *reinterpret_cast<u32x2 *>(op + 32 * c + 8 * g + 4 * hh) = w;
       }
+    }
+  }
+}
+
+// bf16 caches, 64 keys per step (four 16-token tiles, one copied by each
+// wave). Workgroup and lanes as in prefill_gqa32_kernel with one block of 32
+// queries per wave; what changes is the step. Per step and wave:
+//   S^T for keys 0..31 and 32..63 of the step    two chains of D/16 MFMAs
+//                                                 32x32x16 (one per half,
+//                                                 interleaved: a chain never
+//                                                 waits on itself)
+//   one row maximum, one rescale test            over the 64 keys
+//   P V^T                                        4 x D/32 MFMAs 32x32x16
+//   copies of the wave's tile: V of this step,  one buffer resource per
+//   K of the next                                 cache, PIECES/64 copies with
+//                                                 a uniform offset each
+// so the per-step costs (barrier, waits, loop and mask tests, the maximum's
+// cross-lane swap) and the per-tile block lookup fall on twice the MFMAs of
+// a 32-key step. Each half keeps the key permutation of the 32-key kernel
+// (score r of lane l is key 16 (r/8) + 8 (l/32) + r % 8 of the half, the PV
+// B operand as it stands), and the row sum is taken on the packed bf16
+// probabilities the PV products consume (v_dot2c_f32_bf16 against 1.0, two
+// per instruction). A block id outside [0, num_blocks) reads block 0: no
+// access leaves the cache, and that sequence's output is unspecified.
+// LDS: K in two step slots (the next step's K lands during this step), V in
+// one (a step's V is copied at its start and lands during its QK and
+// softmax; a second barrier per step separates the softmax from the PV
+// products): 48 KB at d=128, so three workgroups share a CU.
+template <int D>
+__global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa64_kernel(
+    const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const uint16_t *__restrict__ q, int64_t q_st,
+    int64_t q_sh, uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
+    const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
+    int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
+  using LT = LdsTile<D, false>;
+  static_assert(kPrefillWaves == 4, "one tile per wave per 64-key step");
+  static_assert(LT::PIECES % 64 == 0 && LT::KB % 1024 == 0 && D % 64 == 0, "whole copies per lane");
+  constexpr int KB = LT::KB, VB = LT::VB;  // bytes of one tile's K, V
+  constexpr int CPT = LT::PIECES / 64;     // 16-byte copies per lane per tile
+  constexpr int NK = KB / 1024;            // of which the first NK are K
+  constexpr int DV = D / 64;               // V copies per token octet
+  __shared__ __attribute__((aligned(16))) uint8_t ldsk[2 * 4 * KB];  // K: two steps of four tiles
+  __shared__ __attribute__((aligned(16))) uint8_t ldsv[4 * VB];      // V: one step
+  const int id = blockIdx.x;
+  const int item = (id / (8 * n_qt)) * 8 + (id & 7);
+  const int qt = __builtin_amdgcn_readfirstlane(n_qt - 1 - (id / 8) % n_qt);
+  if (item >= n_items) return;
+  const int b = __builtin_amdgcn_readfirstlane(item / (Hkv * n_hg));
+  const int kvh = __builtin_amdgcn_readfirstlane((item / n_hg) % Hkv);
+  const int hg = item % n_hg;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
+  const int q0 = cu_q[b];
+  const int qlen = cu_q[b + 1] - q0;
+  int L = seq_lens[b];
+  L = L < max_seq ? L : max_seq;
+  const int t0 = qt * 32;
+  if (t0 >= qlen) return;  // the whole workgroup leaves together
+  const int h_local = hg * kPrefillWaves + wave;
+  const bool active = h_local < G;  // an idle wave still copies its tile of every step
+  const int h = kvh * G + (active ? h_local : 0);
+  const int ctx = L - qlen;
+
+  // Q^T operand j: lane l holds d = 16 j + 8 (l/32) .. + 7 of query t0 + l % 32.
+  bf16x8 qb[D / 16];
+  {
+    const int tok = t0 + n;
+    const bool valid = active && tok < qlen;
+    const uint16_t *qp = q + static_cast<int64_t>(q0 + (tok < qlen ? tok : t0)) * q_st + static_cast<int64_t>(h) * q_sh;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+      u32x4 w = *reinterpret_cast<const u32x4 *>(qp + 16 * j + 8 * hh);
+      if (!valid) w = u32x4{0u, 0u, 0u, 0u};
+      qb[j] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+  floatx16 o[D / 32];
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[c][r] = 0.f;
+  float m_ref = -INFINITY, l_part = 0.f;
+
+  const int last = (t0 + 32 < qlen ? t0 + 32 : qlen) - 1;
+  const int kend = ctx + last + 1;  // keys [0, kend)
+  const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
+  const int n_steps = (n_tiles + 3) / 4;
+  const int region = D * BS * 2;
+
+  // Copy k of lane l moves piece p = 64 k + l of the wave's tile (LDS offset
+  // 16 p). K piece p: chunk p >> 4, token p & 15, at ((p >> 4) BS + (p & 15)) 16
+  // of the (block, head) K region = lane part ((l >> 4) BS + (l & 15)) 16 +
+  // copy part 64 BS k. V piece v = p - KB/16: row v % D, octet v / D, at
+  // (v % D) BS 2 + 16 (v / D) = lane part 2 BS l + copy part 128 BS (k' % DV) +
+  // 16 (k' / DV), k' = k - NK. The tile's first token o0 goes into the base.
+  const uint32_t lane_k = static_cast<uint32_t>(((lane >> 4) * BS + (lane & 15)) * 16);
+  const uint32_t lane_v = static_cast<uint32_t>(lane * BS * 2);
+  uint32_t coff[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k)
+    coff[k] = k < NK ? static_cast<uint32_t>(64 * BS * k)
+                     : static_cast<uint32_t>(128 * BS * ((k - NK) % DV) + 16 * ((k - NK) / DV));
+  const uint32_t ldsk0 = lds_addr(ldsk), ldsv0 = lds_addr(ldsv);
+  // This wave's tile of step s is tile 4 s + wave: token 64 s + 16 wave, in
+  // block bix at offset o0, both advanced by 64 tokens per step.
+  const int32_t *btrow = bt + b * bt_stride;
+  int bix = (16 * wave) / BS;
+  int o0 = 16 * wave - bix * BS;
+  const int dbix = 64 / BS, do0 = 64 - dbix * BS;
+  int wbase = 0;  // the window: lane i holds the id of block wbase + i
+  int win = load_i32_drained(btrow, lane, Mb);
+  int64_t vbase = 0;  // V of the wave's tile of the step whose K went out last: cache offset
+  // K of the wave's tile of step s into K slot `slot` (and its V offset kept for issue_v)
+  auto issue_k = [&](int s, int slot) {
+    if (4 * s + wave < n_tiles) {  // uniform
+      if (bix - wbase >= 64) {     // at most once per 64 blocks (its wait drains the copies in flight)
+        wbase += 64;
+        win = load_i32_drained(btrow, wbase + lane, Mb);
+      }
+      int blk = __builtin_amdgcn_readlane(win, bix - wbase);
+      if (!(blk >= 0 && blk < NB)) blk = 0;
+      const int64_t rb = static_cast<int64_t>(blk * Hkv + kvh) * region;
+      vbase = rb + o0 * 2;
+      const __amdgpu_buffer_rsrc_t kr =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(kc + rb + o0 * 16), 0, region, kRawBufferWord3);
+      const uint32_t dst = ldsk0 + static_cast<uint32_t>((4 * slot + wave) * KB);
+#pragma unroll
+      for (int k = 0; k < NK; ++k) buffer_copy16_to_lds(kr, lane_k, coff[k], dst + 1024 * k);
+    }
+    o0 += do0;
+    bix += dbix;
+    if (o0 >= BS) {
+      o0 -= BS;
+      ++bix;
+    }
+  };
+  // V of the wave's tile of step s (whose K went out last) into the V slot
+  auto issue_v = [&](int s) {
+    if (4 * s + wave < n_tiles) {
+      const __amdgpu_buffer_rsrc_t vr =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(vc + vbase), 0, region, kRawBufferWord3);
+      const uint32_t dst = ldsv0 + static_cast<uint32_t>(wave * VB);
+#pragma unroll
+      for (int k = NK; k < CPT; ++k) buffer_copy16_to_lds(vr, lane_v, coff[k], dst + 1024 * (k - NK));
+    }
+  };
+  // Row n of each half's S^T carries key kperm(n) of the half.
+  const int kn = (n & 16) | (((n >> 2) & 3) == 1 ? (n & 3) + 8 : ((n >> 2) & 3) == 2 ? (n & 3) + 4 : (n & 15));
+  const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+
+  if (n_steps > 0) {
+    issue_k(0, 0);
+    wait_vmcnt<0>();
+    barrier_lds();
+    for (int s = 0; s < n_steps; ++s) {
+      const int cur = s & 1;
+      issue_v(s);  // its slot was left at the last barrier
+      const bool k_next = s + 1 < n_steps && 4 * (s + 1) + wave < n_tiles;  // uniform
+      if (s + 1 < n_steps) issue_k(s + 1, cur ^ 1);
+      const int kb = 64 * s;  // position of the step's first key
+      uint32_t pw[4][4];      // PV B operands, packed bf16 probabilities
+      if (active) {
+        floatx16 s0, s1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
+        const uint8_t *lk = ldsk + (cur * 4 + (kn >> 4)) * KB + (kn & 15) * 16;
+#pragma unroll
+        for (int jj = 0; jj < D / 16; ++jj) {
+          const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + (2 * jj + hh) * 256));
+          const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + 2 * KB + (2 * jj + hh) * 256));
+          s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qb[jj], s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qb[jj], s1, 0, 0, 0);
+        }
+        const int min_pos = ctx + t0;  // the smallest query position of the workgroup
+        if (!(kend >= kb + 64 && kb + 63 <= min_pos)) {  // uniform: masks in this step
+          // keys of the step this lane's query sees: 0 .. lim (relative to kb and
+          // to this lane's key octet); past kend nothing is seen
+          const int pos = min_pos + n;
+          const int lim = (pos < kend - 1 ? pos : kend - 1) - kb - 8 * hh;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if (16 * (r / 8) + (r % 8) > lim) s0[r] = -INFINITY;
+            if (32 + 16 * (r / 8) + (r % 8) > lim) s1[r] = -INFINITY;
+          }
+        }
+        float mt = fmaxf(s0[0], s1[0]);
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
+        {
+          const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+          mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1])) * scale_log2;  // the scale is positive
+        }
+        const bool move = mt > m_ref + SOFTMAX_TAU;
+        const float m_new = move ? mt : m_ref;
+        const float corr = (move && m_ref != -INFINITY) ? fast_exp2(m_ref - m_new) : 1.f;
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s0[r] = fast_exp2(__builtin_fmaf(s0[r], scale_log2, -m_use));  // masked: -inf -> 0
+          s1[r] = fast_exp2(__builtin_fmaf(s1[r], scale_log2, -m_use));
+        }
+        // Tile t = 2 half + st takes scores 8 st .. 8 st + 7 of its half, packed
+        // as four words. The words stay scalars until the MFMA operand is
+        // built: the dot products read them one by one (with the words as
+        // elements of a 4-vector, hipcc 7.2 fed every dot product of a vector
+        // its first element).
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const floatx16 &sv = t < 2 ? s0 : s1;
+          const int e0 = 8 * (t & 1);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pw[t][i] = pack_bf16x2(sv[e0 + 2 * i], sv[e0 + 2 * i + 1]);
+        }
+        float ps = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[t][i]), ones, ps, false);
+        l_part = l_part * corr + ps;
+        m_ref = m_new;
+        if (__any(corr != 1.f)) {
+#pragma unroll
+          for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[c][r] *= corr;
+        }
+      }
+      if (k_next)
+        wait_vmcnt<NK>();  // this step's V landed (the next step's K may be in flight)
+      else
+        wait_vmcnt<0>();
+      barrier_lds();  // ... for every wave
+      if (active) {
+        const uint8_t *lv = ldsv + hh * D * 16 + n * 16;  // octet hh: keys 8 hh .. 8 hh + 7 of a tile
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          int vt = kend - kb - 16 * t;  // keys of tile t
+          vt = vt < 0 ? 0 : (vt > 16 ? 16 : vt);
+          if (vt == 0) continue;  // uniform: a tile past the keys (its LDS buffer is stale)
+          const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[t][0], pw[t][1], pw[t][2], pw[t][3]}));
+#pragma unroll
+          for (int c = 0; c < D / 32; ++c) {
+            u32x4 w = *reinterpret_cast<const u32x4 *>(lv + t * VB + 32 * c * 16);
+            if (vt < 16) {  // uniform: slots past the keys may hold NaN
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                if (8 * hh + e >= vt) w[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+            }
+            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb, o[c], 0, 0, 0);
+          }
+        }
+      }
+      wait_vmcnt<0>();  // the next step's K landed
+      barrier_lds();    // ... for every wave; every wave is done with this step's K and V
+    }
+  }
+  const int tok = t0 + n;
+  if (!active || tok >= qlen) return;
+  float l = l_part;
+  {
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t *op = out + static_cast<int64_t>(q0 + tok) * o_st + static_cast<int64_t>(h) * o_sh;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {  // d = 32 c + 8 g + 4 hh + 0..3
+      const u32x2 w = {pack_bf16x2(o[c][4 * g] * inv, o[c][4 * g + 1] * inv),
+                       pack_bf16x2(o[c][4 * g + 2] * inv, o[c][4 * g + 3] * inv)};
+      *reinterpret_cast<u32x2 *>(op + 32 * c + 8 * g + 4 * hh) = w;
     }
   }
 }
@@ -670,7 +975,7 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
       cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS,           \
       cache->num_blocks, scale_log2, n_qt, static_cast<int>(n_items))
 #define WKV_PREFILL32(Dv)                                                                                         \
-  prefill_gqa32_kernel<Dv, prefill_query_blocks<Dv>()><<<grid, 64 * kPrefillWaves, 0, s>>>(                     \
+  prefill_gqa64_kernel<Dv><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                  \
       kc, vc, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h, cu_seqlens_q, seq_lens, block_table,   \
       bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS, cache->num_blocks, scale_log2, n_qt,             \
       static_cast<int>(n_items))

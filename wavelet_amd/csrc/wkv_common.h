@@ -15,6 +15,7 @@ namespace wkv {
 // Vector types matching the MFMA builtin operand types.
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4;
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float floatx2;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16;
