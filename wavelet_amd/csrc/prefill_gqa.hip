@@ -722,11 +722,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa64_kernel(
   // 16 (k' / DV), k' = k - NK. The tile's first token o0 goes into the base.
   const uint32_t lane_k = static_cast<uint32_t>(((lane >> 4) * BS + (lane & 15)) * 16);
   const uint32_t lane_v = static_cast<uint32_t>(lane * BS * 2);
-  uint32_t coff[CPT];
-#pragma unroll
-  for (int k = 0; k < CPT; ++k)
-    coff[k] = k < NK ? static_cast<uint32_t>(64 * BS * k)
-                     : static_cast<uint32_t>(128 * BS * ((k - NK) % DV) + 16 * ((k - NK) / DV));
+  const int nb = static_cast<int>(NB);  // num_blocks * num_kv_heads < 2^31 (checked by the host)
   const uint32_t ldsk0 = lds_addr(ldsk), ldsv0 = lds_addr(ldsv);
   // This wave's tile of step s is tile 4 s + wave: token 64 s + 16 wave, in
   // block bix at offset o0, both advanced by 64 tokens per step.
@@ -745,14 +741,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa64_kernel(
         win = load_i32_drained(btrow, wbase + lane, Mb);
       }
       int blk = __builtin_amdgcn_readlane(win, bix - wbase);
-      if (!(blk >= 0 && blk < NB)) blk = 0;
+      if (!(blk >= 0 && blk < nb)) blk = 0;
       const int64_t rb = static_cast<int64_t>(blk * Hkv + kvh) * region;
       vbase = rb + o0 * 2;
+      // copy part of K copy k: 64 BS k (recomputed here, not held in registers)
+      uint32_t kst = static_cast<uint32_t>(64 * BS);
+      asm volatile("" : "+s"(kst));
       const __amdgpu_buffer_rsrc_t kr =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(kc + rb + o0 * 16), 0, region, kRawBufferWord3);
       const uint32_t dst = ldsk0 + static_cast<uint32_t>((4 * slot + wave) * KB);
 #pragma unroll
-      for (int k = 0; k < NK; ++k) buffer_copy16_to_lds(kr, lane_k, coff[k], dst + 1024 * k);
+      for (int k = 0; k < NK; ++k) buffer_copy16_to_lds(kr, lane_k, kst * k, dst + 1024 * k);
     }
     o0 += do0;
     bix += dbix;
@@ -767,8 +766,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa64_kernel(
       const __amdgpu_buffer_rsrc_t vr =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(vc + vbase), 0, region, kRawBufferWord3);
       const uint32_t dst = ldsv0 + static_cast<uint32_t>(wave * VB);
+      // copy part of V copy k' = k - NK: 128 BS (k' % DV) + 16 (k' / DV)
+      uint32_t vst = static_cast<uint32_t>(128 * BS);
+      asm volatile("" : "+s"(vst));
 #pragma unroll
-      for (int k = NK; k < CPT; ++k) buffer_copy16_to_lds(vr, lane_v, coff[k], dst + 1024 * (k - NK));
+      for (int k = NK; k < CPT; ++k)
+        buffer_copy16_to_lds(vr, lane_v, vst * ((k - NK) % DV) + 16 * ((k - NK) / DV), dst + 1024 * (k - NK));
     }
   };
   // Row n of each half's S^T carries key kperm(n) of the half.
@@ -810,21 +813,54 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa64_kernel(
             if (32 + 16 * (r / 8) + (r % 8) > lim) s1[r] = -INFINITY;
           }
         }
-        float mt = fmaxf(s0[0], s1[0]);
+        if (s == 0) {  // uniform: the reference maximum starts at the first step's row maximum
+          // (every query sees key 0, so it is finite)
+          float mt = fmaxf(s0[0], s1[0]);
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
-        {
+          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
           const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
           mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1])) * scale_log2;  // the scale is positive
+          m_ref = mt == -INFINITY ? 0.f : mt;
         }
-        const bool move = mt > m_ref + SOFTMAX_TAU;
-        const float m_new = move ? mt : m_ref;
-        const float corr = (move && m_ref != -INFINITY) ? fast_exp2(m_ref - m_new) : 1.f;
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        // Exponents against the reference maximum; their maximum (of FMA results,
+        // which max3 takes as they are) says whether it must move.
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          s0[r] = fast_exp2(__builtin_fmaf(s0[r], scale_log2, -m_use));  // masked: -inf -> 0
-          s1[r] = fast_exp2(__builtin_fmaf(s1[r], scale_log2, -m_use));
+          s0[r] = __builtin_fmaf(s0[r], scale_log2, -m_ref);  // masked: -inf
+          s1[r] = __builtin_fmaf(s1[r], scale_log2, -m_ref);
+        }
+        // two chains of max3 over the 32 exponents
+        float mt0 = fmaxf(s0[0], s0[1]), mt1 = fmaxf(s1[0], s1[1]);
+#pragma unroll
+        for (int r = 2; r < 16; r += 2) {
+          mt0 = fmaxf(fmaxf(mt0, s0[r]), s0[r + 1]);
+          mt1 = fmaxf(fmaxf(mt1, s1[r]), s1[r + 1]);
+        }
+        float mt = fmaxf(mt0, mt1);
+        {
+          const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+          mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+        }
+        const bool move = mt > SOFTMAX_TAU;
+        if (__any(move)) {  // rare: some row's maximum rose past the reference by 2^SOFTMAX_TAU
+          const float sh = move ? mt : 0.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            s0[r] -= sh;
+            s1[r] -= sh;
+          }
+          const float corr = fast_exp2(-sh);
+          l_part *= corr;
+          m_ref += sh;
+#pragma unroll
+          for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[c][r] *= corr;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s0[r] = fast_exp2(s0[r]);  // masked: -inf -> 0
+          s1[r] = fast_exp2(s1[r]);
         }
         // Tile t = 2 half + st takes scores 8 st .. 8 st + 7 of its half, packed
         // as four words. The words stay scalars until the MFMA operand is
@@ -844,36 +880,42 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa64_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[t][i]), ones, ps, false);
-        l_part = l_part * corr + ps;
-        m_ref = m_new;
-        if (__any(corr != 1.f)) {
-#pragma unroll
-          for (int c = 0; c < D / 32; ++c)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[c][r] *= corr;
-        }
+        l_part += ps;
       }
       if (k_next)
         wait_vmcnt<NK>();  // this step's V landed (the next step's K may be in flight)
       else
         wait_vmcnt<0>();
+      {
+        // The slots of a partial tile past the keys may hold NaN (0 x NaN in a
+        // PV product is NaN): the wave that copied the tile zeroes them, so
+        // the PV products read V as it stands.
+        int vt = kend - kb - 16 * wave;  // keys of this wave's tile
+        vt = vt < 0 ? 0 : (vt > 16 ? 16 : vt);
+        if (vt > 0 && vt < 16) {  // uniform; at most once per workgroup
+#pragma unroll
+          for (int i = 0; i < D / 32; ++i) {
+            const int pc = 64 * i + lane;  // V piece: octet pc / D, row pc % D (8 tokens)
+            const int cnt = vt - 8 * (pc / D);  // tokens of the piece that are keys
+            u32x4 *ptr = reinterpret_cast<u32x4 *>(ldsv + wave * VB + pc * 16);
+            u32x4 w = *ptr;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (e >= cnt) w[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+            *ptr = w;
+          }
+        }
+      }
       barrier_lds();  // ... for every wave
       if (active) {
         const uint8_t *lv = ldsv + hh * D * 16 + n * 16;  // octet hh: keys 8 hh .. 8 hh + 7 of a tile
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          int vt = kend - kb - 16 * t;  // keys of tile t
-          vt = vt < 0 ? 0 : (vt > 16 ? 16 : vt);
-          if (vt == 0) continue;  // uniform: a tile past the keys (its LDS buffer is stale)
+          if (kend - kb - 16 * t <= 0) continue;  // uniform: a tile past the keys (its LDS buffer is stale)
           const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[t][0], pw[t][1], pw[t][2], pw[t][3]}));
 #pragma unroll
           for (int c = 0; c < D / 32; ++c) {
-            u32x4 w = *reinterpret_cast<const u32x4 *>(lv + t * VB + 32 * c * 16);
-            if (vt < 16) {  // uniform: slots past the keys may hold NaN
-#pragma unroll
-              for (int e = 0; e < 8; ++e)
-                if (8 * hh + e >= vt) w[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-            }
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(lv + t * VB + 32 * c * 16);
             o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb, o[c], 0, 0, 0);
           }
         }
