@@ -362,8 +362,8 @@ def workload(args, torch, dev) -> dict:
         return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
                 # the append kernel wkv_append(_fp8) picks for T = 16,384 tokens: the bulk paths
                 # from 256 (bf16) / 64 (fp8) tokens on
-                "kernel": ("prefill_gqa_fp8_kernel<128> (+ append_fp8_bulk_kernel)" if fp8 else
-                           "prefill_gqa_bf16_kernel<128> (+ append_bf16_bulk_kernel)"),
+                "kernel": ("prefill_gqa_kernel<128,true> (+ append_fp8_bulk_kernel)" if fp8 else
+                           "prefill_gqa_kernel<128,false> (+ append_bf16_bulk_kernel)"),
                 "dtype": "bf16" + (" (fp8-e4m3 KV)" if fp8 else ""),
                 "flops_per_layer": flops, "cache_bytes": caches[0].nbytes, "bound": "mfma",
                 "desc": f"Qwen3-4B prompt step: {args.layers} layers x (append + causal prefill attention), "

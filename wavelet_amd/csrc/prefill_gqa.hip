@@ -15,14 +15,12 @@
 // XCD (the dispatcher deals workgroup i to XCD i mod 8): the keys are served
 // from that XCD's L2 instead of being fetched by all eight. The latest (most
 // expensive, causally) query tiles are dispatched first. Keys are copied once
-// per workgroup into LDS by LDS-DMA, in 16-token tiles:
-//   bf16 caches  prefill_gqa_bf16_kernel: 32 queries per wave on 32x32x16
-//                MFMAs, 64 keys (four tiles) per step
-//   fp8 caches   prefill_gqa_fp8_kernel: 16 queries per wave with the decode
-//                kernels' tile arithmetic (gqa_tiles.h), one tile per step,
-//                two in flight
-// Tiles on the causal diagonal mask per lane (column). Every wave finishes its
-// rows: no split-K, no workspace.
+// per workgroup into LDS by LDS-DMA, in 16-token tiles, four per step of 64
+// keys; each wave holds 32 queries and runs 32x32x16 bf16 MFMAs. fp8 tiles
+// are dequantized in LDS (exactly: power-of-two scales) by the wave that
+// copied them, so both dtypes share the attention arithmetic. Tiles on the
+// causal diagonal mask per lane (column). Every wave finishes its rows: no
+// split-K, no workspace.
 #include "gqa_tiles.h"
 #include "lds_dma.h"
 
@@ -32,200 +30,31 @@ namespace wkv {
 
 constexpr int kPrefillWaves = 4;
 
-// One 16-token key tile of one (block, KV head) in LDS: K as the cache holds
-// it, [D/x chunks][16 tokens][16 bytes]; fp8 V as the cache holds it, [D rows]
-// [16 tokens]; bf16 V as [2 token octets][D rows][8 tokens] (16-byte pieces,
-// so the copy still moves whole pieces). A lane's MFMA operand is one 16-byte
-// LDS read: K, 16 bytes of one token's chunk; bf16 V, the 8 tokens of one
-// octet of one row; fp8 V, a whole row.
-template <int D, bool FP8>
+// Eight e4m3fn codes (bytes of lo, then hi) times a power-of-two scale as
+// eight bf16 values, by the hardware pair conversion (exact: every such
+// product is a bf16 value).
+__device__ __forceinline__ u32x4 fp8x8_to_bf16_words(uint32_t lo, uint32_t hi, float sc) {
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, sc, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, sc, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, sc, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, sc, true))};
+}
+
+// One 16-token key tile of one (block, KV head) in LDS, as the MFMAs read it
+// (bf16; fp8 tiles are dequantized into the same layout): K as a bf16 cache
+// holds it, [D/8 chunks][16 tokens][16 bytes]; V as [2 token octets][D rows]
+// [8 tokens] (16-byte pieces, so a copy still moves whole pieces). A lane's
+// MFMA operand is one 16-byte LDS read: 16 bytes of one token's K chunk, or
+// the 8 tokens of one octet of one V row.
+template <int D>
 struct LdsTile {
-  static constexpr int ESZ = FP8 ? 1 : 2;
-  static constexpr int KB = D * 16 * ESZ;  // K bytes
-  static constexpr int VB = D * 16 * ESZ;  // V bytes
-  static constexpr int BYTES = KB + VB;
-  static constexpr int PIECES = BYTES / 16;  // 16-byte pieces
-  static constexpr int PER_THREAD = (PIECES + 64 * kPrefillWaves - 1) / (64 * kPrefillWaves);
-  static constexpr bool EVEN = PIECES % (64 * kPrefillWaves) == 0;  // else the last round is partial
-  // A wave issues PER_THREAD copies per tile, or none (its waits count on it).
-  static_assert(EVEN || PIECES < 64 * kPrefillWaves, "copies per wave: PER_THREAD or 0");
-  static_assert(PIECES % 64 == 0, "whole wave instructions");
+  static constexpr int KB = D * 16 * 2;  // K bytes
+  static constexpr int VB = D * 16 * 2;  // V bytes
 };
 
-// Global address of 16-byte piece p of the tile (tokens o0..o0+15 of block
-// blk, KV head kvh) and its LDS offset (= 16 p).
-template <int D, bool FP8>
-__device__ __forceinline__ const uint8_t *tile_piece(const uint8_t *kc, const uint8_t *vc, int64_t rbase, int o0,
-                                                     int BS, int p) {
-  using T = LdsTile<D, FP8>;
-  if (p < T::KB / 16) {  // K chunk c, token m: 16 bytes at ((c*BS + o0 + m) * 16) of the region
-    const int c = p >> 4, m = p & 15;
-    return kc + rbase + (static_cast<int64_t>(c) * BS + o0 + m) * 16;
-  }
-  // V row d: the 16 tokens are 32 (bf16) or 16 (fp8) contiguous bytes;
-  // bf16 piece v holds octet v / D of row v % D
-  const int v = p - T::KB / 16;
-  const int d = FP8 ? v : v % D, half = FP8 ? 0 : v / D;
-  return vc + rbase + (static_cast<int64_t>(d) * BS + o0) * T::ESZ + half * 16;
-}
-
-// fp8 caches: 16-token query tiles, 16x16 MFMAs, K and V dequantized per
-// tile by the decode kernels' arithmetic; three LDS buffers, one attended and
-// two in flight.
-template <int D>
-__global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_fp8_kernel(
-    const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const float *__restrict__ ks,
-    const float *__restrict__ vs, const uint16_t *__restrict__ q, int64_t q_st, int64_t q_sh,
-    uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
-    const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
-    int Hkv, int G, int n_hg, int BS, int64_t NB, float scale_log2, int n_qt, int n_items) {
-  constexpr bool FP8 = true;
-  using LT = LdsTile<D, FP8>;
-  constexpr int NBUF = 3;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[NBUF][LT::BYTES];
-  // Linear id = ((item / 8) * n_qt + (n_qt - 1 - qt)) * 8 + item % 8, item =
-  // (sequence, KV head, head group): the XCD (id % 8) depends on the item only.
-  const int id = blockIdx.x;
-  const int item = (id / (8 * n_qt)) * 8 + (id & 7);
-  const int qt = __builtin_amdgcn_readfirstlane(n_qt - 1 - (id / 8) % n_qt);
-  if (item >= n_items) return;
-  const int b = __builtin_amdgcn_readfirstlane(item / (Hkv * n_hg));
-  const int kvh = __builtin_amdgcn_readfirstlane((item / n_hg) % Hkv);
-  const int hg = item % n_hg;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-  const int q0 = cu_q[b];
-  const int qlen = cu_q[b + 1] - q0;
-  int L = seq_lens[b];
-  L = L < max_seq ? L : max_seq;
-  const int t0 = qt * 16;
-  if (t0 >= qlen) return;  // the whole workgroup leaves together
-  const int h_local = hg * kPrefillWaves + wave;
-  const bool active = h_local < G;  // an idle wave still loads its share of every tile
-  const int h = kvh * G + (active ? h_local : 0);
-  const int ctx = L - qlen;  // position of new token 0 (negative only for inconsistent inputs)
-  const int tok = t0 + col;
-  const bool valid = active && tok < qlen;
-  const int pos = ctx + tok;  // this column's position; it sees keys [0, pos]
-
-  bf16x8 qop[D / 32];
-  load_q<D, FP8>(qop, q + static_cast<int64_t>(q0 + (tok < qlen ? tok : t0)) * q_st + static_cast<int64_t>(h) * q_sh,
-                 valid, grp);
-  DecodeState<D, FP8> st;
-#pragma unroll
-  for (int n = 0; n < D / 16; ++n) st.o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
-  st.l = 0.f;
-
-  // Keys up to the tile's last query: [0, kend), in 16-token tiles.
-  const int last = (t0 + 16 < qlen ? t0 + 16 : qlen) - 1;
-  const int kend = ctx + last + 1;
-  const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
-  const int region = D * BS * LT::ESZ;
-  // Tile i's block (a wave-uniform table read: a scalar load, which waits on
-  // its own counter and never on the tile copies in flight), region base and
-  // position.
-  auto tile_src = [&](int i, int64_t &rbase, int &o0, int &blk_ok, float &ksc, float &vsc) {
-    const int ts = 16 * i;
-    const int bi = ts / BS;
-    int blk = bi < Mb ? bt[b * bt_stride + bi] : -1;
-    blk_ok = (blk >= 0 && blk < NB) ? 1 : 0;
-    if (!blk_ok) blk = 0;
-    rbase = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(blk * Hkv + kvh)) * region;
-    o0 = ts % BS;
-    ksc = vsc = 1.f;
-    if constexpr (FP8) {
-      ksc = ks[static_cast<int64_t>(blk) * Hkv + kvh];
-      vsc = vs[static_cast<int64_t>(blk) * Hkv + kvh];
-    }
-  };
-
-  // Tiles are copied HBM -> LDS by LDS-DMA (no register staging): wave w's
-  // k-th copy moves pieces 256 k + 64 w .. + 63, lane i piece 256 k + 64 w + i,
-  // to LDS offset 16 * piece. Tile i + 2 is issued at the start of iteration i
-  // into the buffer tile i - 1 left; before the barrier that publishes tile
-  // i + 1 each wave waits for its own copies of it.
-  const int wave_base = 64 * wave;
-  int okr[NBUF];
-  float kscr[NBUF], vscr[NBUF];
-  auto issue = [&](int i, int bi) {
-    int64_t rbase;
-    int o0;
-    tile_src(i, rbase, o0, okr[bi], kscr[bi], vscr[bi]);
-    const uint32_t dst = lds_addr(&lds[bi][0]);
-#pragma unroll
-    for (int k = 0; k < LT::PER_THREAD; ++k) {
-      const int p0 = 256 * k + wave_base;  // uniform: this wave instruction's first piece
-      if (LT::EVEN || p0 < LT::PIECES)
-        copy16_to_lds(tile_piece<D, FP8>(kc, vc, rbase, o0, BS, p0 + lane),
-                      __builtin_amdgcn_readfirstlane(dst + 16 * p0));
-    }
-  };
-  // Tile i from LDS buffer bi into registers; its column limit in `lim`.
-  auto read_tile = [&](int i, int bi, Tile<D, FP8> &t, int &lim) {
-    const uint8_t *lk = &lds[bi][0];
-    const uint8_t *lv = &lds[bi][LT::KB];
-#pragma unroll
-    for (int j = 0; j < Tile<D, FP8>::NK; ++j)
-      t.k[j] = *reinterpret_cast<const u32x4 *>(lk + ((4 * j + grp) * 16 + col) * 16);
-#pragma unroll
-    for (int j = 0; j < Tile<D, FP8>::NPV / 4; ++j)
-      t.v4[j] = *reinterpret_cast<const u32x4 *>(lv + (64 * j + 16 * grp + col) * 16);
-    const int ts = 16 * i;
-    t.ts = ts;
-    t.valid = (i < n_tiles && okr[bi]) ? ((kend - ts) < 16 ? (kend - ts) : 16) : 0;
-    t.ksc = kscr[bi];
-    t.vsc = vscr[bi];
-    lim = pos - ts + 1;  // keys of the tile this column sees
-    lim = lim < 0 ? 0 : (lim > 16 ? 16 : lim);
-  };
-  auto attend = [&](int i, int bi) {
-    Tile<D, FP8> t;
-    int lim;
-    read_tile(i, bi, t, lim);
-    if (t.valid > 0) attend_tile<D, FP8, true>(st, t, qop, scale_log2, grp, lim);
-  };
-
-  if (n_tiles > 0) {
-    issue(0, 0);
-    if (n_tiles > 1) {
-      issue(1, 1);
-      wait_vmcnt<LT::PER_THREAD>();  // tile 0 landed
-    } else {
-      wait_vmcnt<0>();
-    }
-    barrier_lds();
-    int bi = 0;  // buffer of tile i
-    for (int i = 0; i < n_tiles; ++i) {
-      const int b2 = bi == 0 ? 2 : bi - 1;  // (i + 2) mod 3: the buffer tile i - 1 left
-      const bool more = i + 2 < n_tiles;
-      if (more) issue(i + 2, b2);
-      if (active) attend(i, bi);
-      if (more)
-        wait_vmcnt<LT::PER_THREAD>();  // tile i + 1 landed, tile i + 2 may be in flight
-      else
-        wait_vmcnt<0>();
-      barrier_lds();  // tile i + 1 visible; every wave is done with tile i
-      bi = bi == 2 ? 0 : bi + 1;
-    }
-  }
-  if (!valid) return;
-  float l = st.l + __shfl_xor(st.l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  uint16_t *op = out + static_cast<int64_t>(q0 + tok) * o_st + static_cast<int64_t>(h) * o_sh;
-#pragma unroll
-  for (int n = 0; n < D / 16; ++n) {
-    u32x2 w;
-    w[0] = f32_to_bf16_bits(st.o[n][0] * inv) | (f32_to_bf16_bits(st.o[n][1] * inv) << 16);
-    w[1] = f32_to_bf16_bits(st.o[n][2] * inv) | (f32_to_bf16_bits(st.o[n][3] * inv) << 16);
-    *reinterpret_cast<u32x2 *>(op + 16 * n + 4 * grp) = w;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// bf16 caches: 32 queries per wave on 32x32x16 MFMAs, 64 keys per step (four
-// 16-token tiles, one copied by each wave). Lane l holds query l % 32 in both
+// 32 queries per wave on 32x32x16 MFMAs, 64 keys per step (four 16-token
+// tiles, one copied by each wave). Lane l holds query l % 32 in both
 // accumulators. Per step and wave:
 //   S^T for keys 0..31 and 32..63 of the step    two chains of D/16 MFMAs
 //                                                 32x32x16 (one per half,
@@ -234,35 +63,47 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_gqa_fp8_kernel(
 //   one row maximum, one rescale test            over the 64 keys
 //   P V^T                                        4 x D/32 MFMAs 32x32x16
 //   copies of the wave's tile: V of this step,  one buffer resource per
-//   K of the next                                 cache, PIECES/64 copies with
-//                                                 a uniform offset each
-// so the per-step costs (barrier, waits, loop and mask tests, the maximum's
-// cross-lane swap) and the per-tile block lookup fall on twice the MFMAs of
-// a 32-key step. Each half keeps the key permutation of the 32-key kernel
-// (score r of lane l is key 16 (r/8) + 8 (l/32) + r % 8 of the half, the PV
-// B operand as it stands), and the row sum is taken on the packed bf16
-// probabilities the PV products consume (v_dot2c_f32_bf16 against 1.0, two
-// per instruction). A block id outside [0, num_blocks) reads block 0: no
+//   K of the next                                 cache, 16-byte copies with a
+//                                                 uniform offset each
+// so the per-step costs (barriers, waits, loop and mask tests, the maximum's
+// cross-lane swap) and the per-tile block lookup fall on 32 MFMAs. Row i of
+// each half's S^T carries key kperm(i) of the half (rows 4..7 and 8..11 of
+// each 16 swapped), so score r of lane l is key 16 (r/8) + 8 (l/32) + r % 8
+// of the half -- the PV B operand as it stands -- and the row sum is taken
+// on the packed bf16 probabilities the PV products consume (v_dot2c_f32_bf16
+// against 1.0, two per instruction). A block id outside [0, num_blocks) reads block 0: no
 // access leaves the cache, and that sequence's output is unspecified.
-// LDS: K in two step slots (the next step's K lands during this step), V in
-// one (a step's V is copied at its start and lands during its QK and
-// softmax; a second barrier per step separates the softmax from the PV
-// products): 48 KB at d=128, so three workgroups share a CU.
-template <int D>
-__global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel(
-    const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const uint16_t *__restrict__ q, int64_t q_st,
+// LDS (bf16 caches): K in two step slots (the next step's K lands during
+// this step), V in one (a step's V is copied at its start and lands during
+// its QK and softmax; a second barrier per step separates the softmax from
+// the PV products): 48 KB at d=128, so three workgroups share a CU.
+// fp8 caches: the copies land in a staging area of the copying wave's own,
+// and that wave dequantizes its tile into the bf16 layout above with the
+// hardware conversion at the (block, head) scale (a power of two: exact in
+// bf16) -- its V tile of this step before the first barrier, its K tile of
+// the next step after the PV products, into the single bf16 K slot every wave
+// has left at the first barrier. The attention arithmetic is the bf16 one.
+// LDS: 16 + 16 KB bf16 plus 8 + 8 KB staging at d=128.
+template <int D, bool FP8>
+__global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
+    const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const float *__restrict__ ksc,
+    const float *__restrict__ vsc, const uint16_t *__restrict__ q, int64_t q_st,
     int64_t q_sh, uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
     const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
     int Hkv, int G, int n_hg, int BS, int nb, float scale_log2, int n_qt, int n_items) {
-  using LT = LdsTile<D, false>;
+  using LT = LdsTile<D>;
   static_assert(kPrefillWaves == 4, "one tile per wave per 64-key step");
-  static_assert(LT::PIECES % 64 == 0 && LT::KB % 1024 == 0 && D % 64 == 0, "whole copies per lane");
-  constexpr int KB = LT::KB, VB = LT::VB;  // bytes of one tile's K, V
-  constexpr int CPT = LT::PIECES / 64;     // 16-byte copies per lane per tile
-  constexpr int NK = KB / 1024;            // of which the first NK are K
-  constexpr int DV = D / 64;               // V copies per token octet
-  __shared__ __attribute__((aligned(16))) uint8_t ldsk[2 * 4 * KB];  // K: two steps of four tiles
-  __shared__ __attribute__((aligned(16))) uint8_t ldsv[4 * VB];      // V: one step
+  static_assert(D % 64 == 0, "whole copies per lane");
+  constexpr int KB = LT::KB, VB = LT::VB;   // bytes of one bf16 tile's K, V
+  constexpr int ESZ = FP8 ? 1 : 2;          // cache bytes per element
+  constexpr int NC = D * 16 * ESZ / 1024;   // 16-byte copies per lane of a tile's K (and of its V)
+  constexpr int DV = D / 64;                // bf16 V copies per token octet
+  constexpr int KSLOTS = FP8 ? 1 : 2;       // bf16 K step slots
+  constexpr int SB = FP8 ? D * 16 : 16;     // fp8 staging bytes per tile, K or V
+  __shared__ __attribute__((aligned(16))) uint8_t ldsk[KSLOTS * 4 * KB];  // bf16 K: step slots of four tiles
+  __shared__ __attribute__((aligned(16))) uint8_t ldsv[4 * VB];           // bf16 V: one step
+  __shared__ __attribute__((aligned(16))) uint8_t stgk[4 * SB];           // fp8 K as copied, a tile per wave
+  __shared__ __attribute__((aligned(16))) uint8_t stgv[4 * SB];           // fp8 V as copied
   const int id = blockIdx.x;
   const int item = (id / (8 * n_qt)) * 8 + (id & 7);
   const int qt = __builtin_amdgcn_readfirstlane(n_qt - 1 - (id / 8) % n_qt);
@@ -309,17 +150,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
   const int kend = ctx + last + 1;  // keys [0, kend)
   const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
   const int n_steps = (n_tiles + 3) / 4;
-  const int region = D * BS * 2;
+  const int region = D * BS * ESZ;
 
-  // Copy k of lane l moves piece p = 64 k + l of the wave's tile (LDS offset
-  // 16 p). K piece p: chunk p >> 4, token p & 15, at ((p >> 4) BS + (p & 15)) 16
-  // of the (block, head) K region = lane part ((l >> 4) BS + (l & 15)) 16 +
-  // copy part 64 BS k. V piece v = p - KB/16: row v % D, octet v / D, at
-  // (v % D) BS 2 + 16 (v / D) = lane part 2 BS l + copy part 128 BS (k' % DV) +
-  // 16 (k' / DV), k' = k - NK. The tile's first token o0 goes into the base.
+  // Copy k of lane l moves piece p = 64 k + l of the wave's tile's K or V
+  // (LDS offset 16 p). K piece p (both dtypes: 16-byte chunks): chunk p >> 4,
+  // token p & 15, at ((p >> 4) BS + (p & 15)) 16 of the (block, head) K region
+  // = lane part ((l >> 4) BS + (l & 15)) 16 + copy part 64 BS k. bf16 V piece
+  // p: row p % D, octet p / D, at (p % D) BS 2 + 16 (p / D) = lane part 2 BS l
+  // + copy part 128 BS (k % DV) + 16 (k / DV). fp8 V piece p: row p, at p BS =
+  // lane part BS l + copy part 64 BS k. The tile's first token o0 goes into
+  // the base.
   const uint32_t lane_k = static_cast<uint32_t>(((lane >> 4) * BS + (lane & 15)) * 16);
-  const uint32_t lane_v = static_cast<uint32_t>(lane * BS * 2);
+  const uint32_t lane_v = static_cast<uint32_t>(lane * BS * ESZ);
   const uint32_t ldsk0 = lds_addr(ldsk), ldsv0 = lds_addr(ldsv);
+  const uint32_t stgk0 = lds_addr(stgk), stgv0 = lds_addr(stgv);
+  float ks_next = 1.f, vs_next = 1.f, vs_cur = 1.f;  // fp8 scales of the wave's tiles
   // This wave's tile of step s is tile 4 s + wave: token 64 s + 16 wave, in
   // block bix at offset o0, both advanced by 64 tokens per step.
   const int32_t *btrow = bt + b * bt_stride;
@@ -341,15 +186,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
       // (block, head) region index < 2^31 (checked by the host), times the region
       const int64_t rb = static_cast<int64_t>(static_cast<uint64_t>(static_cast<uint32_t>(blk * Hkv + kvh)) *
                                               static_cast<uint32_t>(region));
-      vbase = rb + o0 * 2;
+      vbase = rb + o0 * ESZ;
+      if constexpr (FP8) {
+        ks_next = ksc[blk * Hkv + kvh];
+        vs_next = vsc[blk * Hkv + kvh];
+      }
       // copy part of K copy k: 64 BS k (recomputed here, not held in registers)
       uint32_t kst = static_cast<uint32_t>(64 * BS);
       asm volatile("" : "+s"(kst));
       const __amdgpu_buffer_rsrc_t kr =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(kc + rb + o0 * 16), 0, region, kRawBufferWord3);
-      const uint32_t dst = ldsk0 + static_cast<uint32_t>((4 * slot + wave) * KB);
+      const uint32_t dst = FP8 ? stgk0 + static_cast<uint32_t>(wave * SB)
+                               : ldsk0 + static_cast<uint32_t>((4 * slot + wave) * KB);
 #pragma unroll
-      for (int k = 0; k < NK; ++k) buffer_copy16_to_lds(kr, lane_k, kst * k, dst + 1024 * k);
+      for (int k = 0; k < NC; ++k) buffer_copy16_to_lds(kr, lane_k, kst * k, dst + 1024 * k);
     }
     o0 += do0;
     bix += dbix;
@@ -363,13 +213,53 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
     if (4 * s + wave < n_tiles) {
       const __amdgpu_buffer_rsrc_t vr =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(vc + vbase), 0, region, kRawBufferWord3);
-      const uint32_t dst = ldsv0 + static_cast<uint32_t>(wave * VB);
-      // copy part of V copy k' = k - NK: 128 BS (k' % DV) + 16 (k' / DV)
-      uint32_t vst = static_cast<uint32_t>(128 * BS);
-      asm volatile("" : "+s"(vst));
+      if constexpr (FP8) {
+        const uint32_t dst = stgv0 + static_cast<uint32_t>(wave * SB);
+        uint32_t vst = static_cast<uint32_t>(64 * BS);  // copy part: 64 BS k
+        asm volatile("" : "+s"(vst));
 #pragma unroll
-      for (int k = NK; k < CPT; ++k)
-        buffer_copy16_to_lds(vr, lane_v, vst * ((k - NK) % DV) + 16 * ((k - NK) / DV), dst + 1024 * (k - NK));
+        for (int k = 0; k < NC; ++k) buffer_copy16_to_lds(vr, lane_v, vst * k, dst + 1024 * k);
+      } else {
+        const uint32_t dst = ldsv0 + static_cast<uint32_t>(wave * VB);
+        uint32_t vst = static_cast<uint32_t>(128 * BS);  // copy part: 128 BS (k % DV) + 16 (k / DV)
+        asm volatile("" : "+s"(vst));
+#pragma unroll
+        for (int k = 0; k < NC; ++k)
+          buffer_copy16_to_lds(vr, lane_v, vst * (k % DV) + 16 * (k / DV), dst + 1024 * k);
+      }
+    }
+  };
+  // fp8: the wave's K tile, staged, into bf16 K slot 0 at scale sc. Piece
+  // p = 64 i + l: chunk c = p >> 4 (16 d), token m = p & 15 -> bf16 chunks
+  // 2c, 2c + 1 of token m.
+  auto convert_k = [&](float sc) {
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) {
+      const int pc = 64 * i + lane;
+      const u32x4 w = *reinterpret_cast<const u32x4 *>(stgk + wave * SB + pc * 16);
+      uint8_t *dk = ldsk + wave * KB + ((2 * (pc >> 4)) * 16 + (pc & 15)) * 16;
+      *reinterpret_cast<u32x4 *>(dk) = fp8x8_to_bf16_words(w[0], w[1], sc);
+      *reinterpret_cast<u32x4 *>(dk + 256) = fp8x8_to_bf16_words(w[2], w[3], sc);
+    }
+  };
+  // fp8: the wave's V tile, staged, into the bf16 V slot at scale sc, tokens
+  // at or past vt zeroed. Piece p = 64 i + l: row p, 16 tokens -> octets 0, 1
+  // of row p.
+  auto convert_v = [&](float sc, int vt) {
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) {
+      const int pc = 64 * i + lane;
+      const u32x4 w = *reinterpret_cast<const u32x4 *>(stgv + wave * SB + pc * 16);
+      u32x4 lo = fp8x8_to_bf16_words(w[0], w[1], sc), hi = fp8x8_to_bf16_words(w[2], w[3], sc);
+      if (vt < 16) {  // uniform: the tile's slots past the keys may hold NaN
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (e >= vt) lo[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+          if (8 + e >= vt) hi[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+        }
+      }
+      *reinterpret_cast<u32x4 *>(ldsv + wave * VB + pc * 16) = lo;
+      *reinterpret_cast<u32x4 *>(ldsv + wave * VB + (D + pc) * 16) = hi;
     }
   };
   // Row n of each half's S^T carries key kperm(n) of the half.
@@ -379,11 +269,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
   if (n_steps > 0) {
     issue_k(0, 0);
     wait_vmcnt<0>();
+    if constexpr (FP8) {
+      if (wave < n_tiles) convert_k(ks_next);  // uniform
+      vs_cur = vs_next;
+    }
     barrier_lds();
     for (int s = 0; s < n_steps; ++s) {
       const int cur = s & 1;
       issue_v(s);  // its slot was left at the last barrier
-      const bool k_next = s + 1 < n_steps && 4 * (s + 1) + wave < n_tiles;  // uniform
+      const bool k_next = s + 1 < n_steps && 4 * (s + 1) + wave < n_tiles;  // uniform: this wave copies K next
       if (s + 1 < n_steps) issue_k(s + 1, cur ^ 1);
       const int kb = 64 * s;  // position of the step's first key
       uint32_t pw[4][4];      // PV B operands, packed bf16 probabilities
@@ -391,7 +285,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
         floatx16 s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
-        const uint8_t *lk = ldsk + (cur * 4 + (kn >> 4)) * KB + (kn & 15) * 16;
+        const uint8_t *lk = ldsk + ((FP8 ? 0 : cur) * 4 + (kn >> 4)) * KB + (kn & 15) * 16;
 #pragma unroll
         for (int jj = 0; jj < D / 16; ++jj) {
           const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + (2 * jj + hh) * 256));
@@ -481,7 +375,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
         l_part += ps;
       }
       if (k_next)
-        wait_vmcnt<NK>();  // this step's V landed (the next step's K may be in flight)
+        wait_vmcnt<NC>();  // this step's V landed (the next step's K may be in flight)
       else
         wait_vmcnt<0>();
       {
@@ -490,7 +384,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
         // the PV products read V as it stands.
         int vt = kend - kb - 16 * wave;  // keys of this wave's tile
         vt = vt < 0 ? 0 : (vt > 16 ? 16 : vt);
-        if (vt > 0 && vt < 16) {  // uniform; at most once per workgroup
+        if (FP8 && vt > 0) {  // uniform
+          convert_v(vs_cur, vt);
+        } else if (!FP8 && vt > 0 && vt < 16) {  // uniform; at most once per workgroup
 #pragma unroll
           for (int i = 0; i < D / 32; ++i) {
             const int pc = 64 * i + lane;  // V piece: octet pc / D, row pc % D (8 tokens)
@@ -519,7 +415,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_bf16_kernel
         }
       }
       wait_vmcnt<0>();  // the next step's K landed
-      barrier_lds();    // ... for every wave; every wave is done with this step's K and V
+      if constexpr (FP8) {
+        if (k_next) convert_k(ks_next);  // every wave left the K slot at the first barrier
+        vs_cur = vs_next;
+      }
+      barrier_lds();  // ... for every wave; every wave is done with this step's K and V
     }
   }
   const int tok = t0 + n;
@@ -586,7 +486,7 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
   const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
   const int n_hg = (G + kPrefillWaves - 1) / kPrefillWaves;
-  const int q_tile = fp8 ? 16 : 32;
+  const int q_tile = 32;
   const int n_qt = (max_query_len + q_tile - 1) / q_tile;
   const int64_t n_items = static_cast<int64_t>(batch) * Hkv * n_hg;
   const int64_t n_wg = (n_items + 7) / 8 * 8 * n_qt;
@@ -598,22 +498,16 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   auto qq = static_cast<const uint16_t *>(q);
   auto oo = static_cast<uint16_t *>(out);
   const float scale_log2 = scale * 1.4426950408889634f;
-#define WKV_PREFILL(Dv)                                                                                           \
-  prefill_gqa_fp8_kernel<Dv><<<grid, 64 * kPrefillWaves, 0, s>>>(                                              \
+#define WKV_PREFILL(Dv, F8)                                                                                       \
+  prefill_gqa_kernel<Dv, F8><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                \
       kc, vc, cache->k_scale, cache->v_scale, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h,       \
       cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS,           \
-      cache->num_blocks, scale_log2, n_qt, static_cast<int>(n_items))
-#define WKV_PREFILL32(Dv)                                                                                         \
-  prefill_gqa_bf16_kernel<Dv><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                  \
-      kc, vc, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h, cu_seqlens_q, seq_lens, block_table,   \
-      bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS, static_cast<int>(cache->num_blocks), scale_log2,  \
-      n_qt, static_cast<int>(n_items))
+      static_cast<int>(cache->num_blocks), scale_log2, n_qt, static_cast<int>(n_items))
   if (D == 128) {
-    if (fp8) WKV_PREFILL(128); else WKV_PREFILL32(128);
+    if (fp8) WKV_PREFILL(128, true); else WKV_PREFILL(128, false);
   } else {
-    if (fp8) WKV_PREFILL(64); else WKV_PREFILL32(64);
+    if (fp8) WKV_PREFILL(64, true); else WKV_PREFILL(64, false);
   }
-#undef WKV_PREFILL32
 #undef WKV_PREFILL
   WKV_CHECK_LAUNCH("paged prefill");
   return WKV_OK;
