@@ -175,3 +175,94 @@ def test_decode_plan_shapes_and_errors():
     assert lib.wkv_decode_plan(64, 8, 4096, 8, 0, ctypes.byref(o), ctypes.byref(o), ctypes.byref(o)) == _lib.WKV_ERR_INVALID
     assert lib.wkv_decode_plan(64, 0, 4096, 16, 0, ctypes.byref(o), ctypes.byref(o), ctypes.byref(o)) == _lib.WKV_ERR_INVALID
     assert lib.wkv_decode_plan(64, 8, 4096, 16, 0, None, ctypes.byref(o), ctypes.byref(o)) == _lib.WKV_ERR_INVALID
+
+
+@host_only
+def test_prefill_rejects_bad_arguments_before_launch():
+    lib = _lib.load()
+    d = _desc()  # 2 KV heads, d=128, blocks of 16
+    base = dict(key=None, kst=0, ksh=0, value=None, vst=0, vsh=0, slots=None, ntok=0, q=16, qst=1024, qsh=128,
+                out=16, ost=1024, osh=128, hq=8, cu=16, sl=16, bt=16, bts=4, mb=4, batch=1, mq=16, ms=64, scale=0.1)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return lib.wkv_prefill_gqa(ctypes.byref(d), a["key"], a["kst"], a["ksh"], a["value"], a["vst"], a["vsh"],
+                                   a["slots"], a["ntok"], a["q"], a["qst"], a["qsh"], a["out"], a["ost"], a["osh"],
+                                   a["hq"], a["cu"], a["sl"], a["bt"], a["bts"], a["mb"], a["batch"], a["mq"],
+                                   a["ms"], a["scale"], None)
+
+    assert call(hq=3) == _lib.WKV_ERR_INVALID  # not a multiple of the KV heads
+    assert call(q=17) == _lib.WKV_ERR_INVALID
+    assert "aligned" in _lib.last_error()
+    assert call(qst=1020) == _lib.WKV_ERR_INVALID  # q strides: multiples of 8
+    assert call(out=None) == _lib.WKV_ERR_INVALID
+    assert call(osh=2) == _lib.WKV_ERR_INVALID  # out strides: multiples of 4
+    assert call(cu=None) == _lib.WKV_ERR_INVALID
+    assert call(bts=2) == _lib.WKV_ERR_INVALID  # table stride below its width
+    assert call(scale=float("inf")) == _lib.WKV_ERR_INVALID
+    assert call(batch=70000) == _lib.WKV_ERR_INVALID
+    assert call(ntok=-1) == _lib.WKV_ERR_INVALID
+    # the append half: a key without a value is rejected before anything runs
+    assert call(key=16, kst=256, ksh=128, slots=16, ntok=4) == _lib.WKV_ERR_INVALID
+    # nothing to attend: a no-op success
+    assert call(batch=0) == _lib.WKV_OK
+    assert call(mq=0) == _lib.WKV_OK
+
+
+@host_only
+def test_grouped_decode_rejects_bad_arguments_before_launch():
+    lib = _lib.load()
+    d = _desc()
+    base = dict(q=16, qsb=1024, qsh=128, out=16, hq=8, bt=16, bts=4, mb=4, sl=16, batch=8, ms=64, pre=16, gs=4,
+                mpl=32, scale=0.1, part=0)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return lib.wkv_paged_decode_gqa_grouped(ctypes.byref(d), None, 0, 0, None, 0, 0, None, a["q"], a["qsb"],
+                                                a["qsh"], a["out"], a["hq"], a["bt"], a["bts"], a["mb"], a["sl"],
+                                                a["batch"], a["ms"], a["pre"], a["gs"], a["mpl"], a["scale"],
+                                                a["part"], None, 0, None, None)
+
+    assert call(hq=3) == _lib.WKV_ERR_INVALID
+    assert call(hq=64) == _lib.WKV_ERR_UNSUPPORTED  # 32 query heads per KV head
+    assert call(pre=None) == _lib.WKV_ERR_INVALID
+    assert "prefix_lens" in _lib.last_error()
+    assert call(gs=0) == _lib.WKV_ERR_INVALID
+    assert call(gs=9) == _lib.WKV_ERR_INVALID  # group larger than the batch
+    assert call(mpl=-1) == _lib.WKV_ERR_INVALID
+    assert call(part=24) == _lib.WKV_ERR_INVALID  # not a multiple of the block size
+    assert call(scale=float("nan")) == _lib.WKV_ERR_INVALID
+    assert call(bt=None) == _lib.WKV_ERR_INVALID
+
+
+@host_only
+def test_sample_gather_copy_reject_bad_arguments_before_launch():
+    lib = _lib.load()
+    s = lib.wkv_sample
+
+    def sample(logits=16, dtype=1, stride=1024, batch=2, vocab=1024, out=16):
+        return s(logits, dtype, stride, batch, vocab, None, None, None, None, None, None, None, 0, out, None, None,
+                 None, None)
+
+    assert sample(vocab=0) == _lib.WKV_ERR_INVALID
+    assert sample(logits=None) == _lib.WKV_ERR_INVALID
+    assert sample(out=None) == _lib.WKV_ERR_INVALID
+    assert sample(dtype=2) == _lib.WKV_ERR_INVALID
+    assert sample(stride=1000) == _lib.WKV_ERR_INVALID  # rows shorter than the vocabulary
+    assert sample(batch=0) == _lib.WKV_OK
+    d = _desc()
+    g = lib.wkv_gather
+
+    def gather(bt=16, bts=4, mb=4, sl=16, cu=16, batch=2, ok=16, ov=16, dq=0):
+        return g(ctypes.byref(d), bt, bts, mb, sl, cu, batch, ok, ov, dq, None)
+
+    assert gather(batch=-1) == _lib.WKV_ERR_INVALID
+    assert gather(bts=2) == _lib.WKV_ERR_INVALID
+    assert gather(bt=None) == _lib.WKV_ERR_INVALID
+    assert gather(ok=17) == _lib.WKV_ERR_INVALID
+    assert gather(dq=2) == _lib.WKV_ERR_INVALID
+    assert gather(dq=1) == _lib.WKV_ERR_INVALID  # dequantizing applies to fp8 caches only
+    assert gather(batch=0) == _lib.WKV_OK
+    assert lib.wkv_copy_blocks(ctypes.byref(d), None, -1, None) == _lib.WKV_ERR_INVALID
+    assert lib.wkv_copy_blocks(ctypes.byref(d), None, 1, None) == _lib.WKV_ERR_INVALID
+    assert lib.wkv_copy_blocks(ctypes.byref(d), None, 0, None) == _lib.WKV_OK

@@ -80,8 +80,22 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source (one object each, in parallel) and link libwkv.so (always rebuilds)."""
+# Host-code sanitizers for a CPU-only check of the C ABI's host side (argument
+# validation, plans, sizes): every -fsanitize= applies to the host compilation
+# only (-Xarch_host); the device code is built as usual. The library links the
+# shared sanitizer runtime, which the process that loads it preloads
+# (asan_runtime()).
+SANITIZE_COMPILE = [
+    "-Xarch_host", "-g",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+]
+SANITIZE_LINK = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined", "-shared-libsan"]
+
+
+def _build(out: Path, compile_extra: list[str], link_extra: list[str], verbose: bool) -> Path:
     cc = hipcc()
     inc = ["-I", str(PKG.parent / "include")]
     with tempfile.TemporaryDirectory(prefix="wkv_build_") as tmpdir:
@@ -90,14 +104,37 @@ def build(verbose: bool = False) -> Path:
         for src in sources():
             obj = Path(tmpdir) / (src.stem + ".o")
             objs.append(obj)
-            cmds.append([cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *inc, "-c", str(src), "-o", str(obj)])
+            cmds.append([cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *compile_extra, *inc, "-c", str(src),
+                         "-o", str(obj)])
         with ThreadPoolExecutor(max_workers=min(8, len(cmds))) as pool:
             for f in [pool.submit(_run, c, verbose) for c in cmds]:
                 f.result()
-        tmp = LIB.with_suffix(".so.tmp")
-        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
-    os.replace(tmp, LIB)
-    return LIB
+        tmp = out.with_suffix(".so.tmp")
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_extra, *map(str, objs), "-o", str(tmp)], verbose)
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source (one object each, in parallel) and link libwkv.so (always rebuilds)."""
+    return _build(LIB, [], [], verbose)
+
+
+def build_sanitized(out: Path, verbose: bool = False) -> Path:
+    """The same library with AddressSanitizer and UndefinedBehaviorSanitizer on its host code, at `out`."""
+    return _build(Path(out), SANITIZE_COMPILE, SANITIZE_LINK, verbose)
+
+
+def asan_runtime() -> Path | None:
+    """The shared AddressSanitizer runtime of the compiler that builds the library (None if absent)."""
+    clang = Path(hipcc()).resolve().parent.parent / "lib" / "llvm" / "bin" / "clang"
+    if not clang.exists():
+        clang = Path(hipcc()).resolve().parent.parent / "llvm" / "bin" / "clang"
+    if not clang.exists():
+        return None
+    proc = subprocess.run([str(clang), "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = Path(proc.stdout.strip())
+    return path if proc.returncode == 0 and path.is_absolute() and path.exists() else None
 
 
 if __name__ == "__main__":
