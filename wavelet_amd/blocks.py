@@ -234,6 +234,9 @@ class BlockManager:
         self._hash_of.clear()
 
     # -- tables ------------------------------------------------------------------
+    def __contains__(self, seq_id) -> bool:
+        return seq_id in self._seqs
+
     def seq_len(self, seq_id) -> int:
         return self._seqs[seq_id].length
 
