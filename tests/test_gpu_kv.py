@@ -142,6 +142,37 @@ def test_append_fp8_bulk_runs(cuda, BS):
          "continued and fresh runs")
 
 
+def test_append_fp8_bulk_whole_blocks_every_pattern(cuda):
+    """Whole fresh 16-token blocks through the bulk kernel (its fast path: 16-byte stores, the
+    hardware code conversion) holding every bf16 pattern -- sorted by magnitude, so blocks span
+    subnormals to infinities, then shuffled, so NaN lands in most blocks (which must take the
+    general path) -- plus a block whose tokens come in reverse slot order: codes and scales
+    bit-exact against the oracle."""
+    NB, BS, H, D = 128, 16, 2, 128
+    kc, vc = paged.empty_cache(NB, BS, H, D, dtype=np.uint8, fill=0xAA)
+    ks = np.zeros((NB, H), np.float32)
+    vs = np.zeros((NB, H), np.float32)
+    cache = PagedKVCache(NB, BS, H, D, kv_dtype="fp8_e4m3", device=cuda)
+    _upload(cache, kc, vc, ks, vs)
+
+    def both(key_bits, val_bits, slots, what):
+        assert len(slots) >= 64  # the bulk kernel's range
+        paged.append_fp8(kc, vc, ks, vs, key_bits, val_bits, slots)
+        cache.append(to_dev_bits(key_bits, BF16, cuda), to_dev_bits(val_bits, BF16, cuda),
+                     torch.from_numpy(np.asarray(slots, np.int64)).to(cuda))
+        _assert_cache_equal(cache, kc, vc, ks, vs, what=what)
+
+    rows = _exhaustive_bf16_rows(H, D)  # [256, 2, 128]
+    whole = np.arange(256, dtype=np.int64)  # blocks 0..15, offsets 0..15 in order
+    both(rows, rows[::-1].copy(), whole, "sorted patterns in whole blocks")
+    rng = np.random.default_rng(7)
+    mixed = rows.reshape(-1)[rng.permutation(rows.size)].reshape(rows.shape)
+    both(mixed, mixed[::-1].copy(), whole + 16 * BS, "shuffled patterns in whole blocks")
+    rev = (32 * BS + np.arange(BS)[::-1]).astype(np.int64)  # one block, tokens in reverse slot order
+    fwd = np.arange(33 * BS, 37 * BS, dtype=np.int64)
+    both(rows[:80], rows[80:160].copy(), np.concatenate([rev, fwd]), "a block in reverse order")
+
+
 def test_append_fp8_bit_exact_exhaustive_and_scale_growth(cuda):
     NB, BS, H, D = 512, 16, 2, 128
     kc, vc = paged.empty_cache(NB, BS, H, D, dtype=np.uint8, fill=0xAA)

@@ -123,4 +123,100 @@ __device__ void fp8_append_run_vec(uint8_t *__restrict__ cache, float *__restric
   if (lane == 0) scales[blk * H + h] = s;
 }
 
+// Codes of a and b (after the clamp to +-448; never NaN here) in bytes
+// 2 w, 2 w + 1 of `old`, by the hardware conversion: for every finite input
+// bit-identical to e4m3_encode (checked on the GPU for all bf16 patterns at
+// several scales). NaN is the one difference -- the hardware codes +NaN 0xFF
+// where e4m3_encode gives 0x7F -- so callers keep NaN off this path.
+template <bool W1>
+__device__ __forceinline__ uint32_t e4m3_pack2(float a, float b, uint32_t old) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, static_cast<int>(old), W1));
+}
+
+// Four bf16 pairs (words w0..w3, low half first) times inv, clamped, as 8 codes
+// in two words.
+__device__ __forceinline__ u32x2 e4m3_pack8(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, float inv) {
+  auto lo = [&](uint32_t w) { return __builtin_amdgcn_fmed3f(__uint_as_float(w << 16) * inv, -448.f, 448.f); };
+  auto hi = [&](uint32_t w) { return __builtin_amdgcn_fmed3f(__uint_as_float(w & 0xffff0000u) * inv, -448.f, 448.f); };
+  u32x2 r;
+  r[0] = e4m3_pack2<true>(lo(w1), hi(w1), e4m3_pack2<false>(lo(w0), hi(w0), 0u));
+  r[1] = e4m3_pack2<true>(lo(w3), hi(w3), e4m3_pack2<false>(lo(w2), hi(w2), 0u));
+  return r;
+}
+
+// fp8 append of a whole fresh block (16 tokens t..t+15 at offsets 0..15 of
+// block blk, block_size 16) for one head, K and V, by one wave -- the prompt
+// case. The block starts afresh (its scale is the run's), so nothing earlier
+// is re-encoded. Returns false, having written nothing, when the block's
+// inputs hold a NaN (the caller then takes fp8_append_run_vec, which codes NaN
+// as e4m3_encode does). K: lane l quantises token l % 16, 16-d chunks
+// l / 16 + 4 j, each one 16-byte store; V: lane l owns d rows RV l .. RV l +
+// RV - 1 (RV = D / 64) and stores each row's 16 tokens as 16 bytes. Each
+// block's absolute maximum is an integer maximum of bf16 magnitude bits (a
+// NaN's bits exceed infinity's). Source rows 16-byte aligned (the host checks).
+template <int D>
+__device__ bool fp8_append_block16(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ ks,
+                                   float *__restrict__ vs, const uint16_t *__restrict__ key, int64_t kst,
+                                   int64_t ksh, const uint16_t *__restrict__ val, int64_t vst, int64_t vsh,
+                                   int64_t t, int64_t blk, int h, int H) {
+  constexpr int BS = 16, NC = D / 64, RV = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int m = lane & 15;
+  u32x4 kw[NC][2];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const uint16_t *p = key + (t + m) * kst + h * ksh + 16 * ((lane >> 4) + 4 * j);
+    kw[j][0] = *reinterpret_cast<const u32x4 *>(p);
+    kw[j][1] = *reinterpret_cast<const u32x4 *>(p + 8);
+  }
+  uint32_t vw[BS];  // token i's RV values of this lane's rows (RV = 2: one word, RV = 1: the low half)
+#pragma unroll
+  for (int i = 0; i < BS; ++i) {
+    const uint16_t *p = val + (t + i) * vst + h * vsh + RV * lane;
+    if constexpr (RV == 2)
+      vw[i] = *reinterpret_cast<const uint32_t *>(p);
+    else
+      vw[i] = *p;
+  }
+  uint32_t ka = 0u, va = 0u;  // largest magnitude bits, as bf16
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = kw[j][q][e];
+        ka = max(ka, max(w & 0x7fffu, (w >> 16) & 0x7fffu));
+      }
+#pragma unroll
+  for (int i = 0; i < BS; ++i) va = max(va, max(vw[i] & 0x7fffu, (vw[i] >> 16) & 0x7fffu));
+  ka = wave_reduce(ka, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+  va = wave_reduce(va, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+  if (ka > 0x7f80u || va > 0x7f80u) return false;  // uniform: a NaN somewhere
+  const float sk = pow2_scale(__uint_as_float(ka << 16)), sv = pow2_scale(__uint_as_float(va << 16));
+  const float ik = 1.0f / sk, iv = 1.0f / sv;  // exact: powers of two
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const u32x2 a = e4m3_pack8(kw[j][0][0], kw[j][0][1], kw[j][0][2], kw[j][0][3], ik);
+    const u32x2 b = e4m3_pack8(kw[j][1][0], kw[j][1][1], kw[j][1][2], kw[j][1][3], ik);
+    *reinterpret_cast<u32x4 *>(kc + fp8_k_index<D>(blk, h, H, BS, m, 16 * ((lane >> 4) + 4 * j))) =
+        u32x4{a[0], a[1], b[0], b[1]};
+  }
+#pragma unroll
+  for (int rr = 0; rr < RV; ++rr) {
+    // row RV lane + rr: the rr-th half of every token's word, 16 tokens
+    auto row = [&](int i) { return (vw[i] >> (16 * rr)) & 0xffffu; };
+    auto pair = [&](int i) { return row(i) | (row(i + 1) << 16); };
+    const u32x2 a = e4m3_pack8(pair(0), pair(2), pair(4), pair(6), iv);
+    const u32x2 b = e4m3_pack8(pair(8), pair(10), pair(12), pair(14), iv);
+    const u32x4 out = {a[0], a[1], b[0], b[1]};
+    *reinterpret_cast<u32x4 *>(vc + fp8_v_index<D>(blk, h, H, BS, 0, RV * lane + rr)) = out;
+  }
+  if (lane == 0) {
+    ks[blk * H + h] = sk;
+    vs[blk * H + h] = sv;
+  }
+  return true;
+}
+
 }  // namespace wkv

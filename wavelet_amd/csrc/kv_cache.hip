@@ -129,11 +129,13 @@ __global__ __launch_bounds__(64) void append_fp8_kernel(uint8_t *__restrict__ kc
 }
 
 // Bulk fp8 append (prompt-sized calls): one wave per (64-token window of the
-// call, KV head). The wave finds the runs that start in its window (a ballot
-// over its 64 slots) and appends each -- K and V, with the same scale rule --
-// with 16-byte loads and K stores; a run that reaches past the window is
-// still this wave's. (One workgroup per token, as the small-call kernel
-// launches, left 15 of 16 idle and each run to dependent 2-byte loads.)
+// call, KV head). The wave finds the runs that start in its window and their
+// lengths from ballots over the blocks of this window's and the next window's
+// tokens (a run lies in one block, so with blocks of at most 64 tokens it ends
+// within the next window), and appends each run -- K and V, with the same
+// scale rule; a run that reaches past the window is still this wave's. A whole
+// fresh 16-token block (the prompt case) takes fp8_append_block16: 16-byte
+// loads and stores, hardware code conversion. Other runs: fp8_append_run_vec.
 constexpr int kFp8BulkMinTokens = 64;
 template <int D>
 __global__ __launch_bounds__(64) void append_fp8_bulk_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
@@ -146,28 +148,53 @@ __global__ __launch_bounds__(64) void append_fp8_bulk_kernel(uint8_t *__restrict
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
   const int h = blockIdx.y;
   const int lane = threadIdx.x;
-  bool start = false;
-  if (t0 + lane < T) {
-    const int64_t slot = slots[t0 + lane];
-    if (slot >= 0 && slot / BS < NB) {
-      const int64_t prev = t0 + lane > 0 ? slots[t0 + lane - 1] : -1;
-      start = !(prev >= 0 && prev / BS == slot / BS);
-    }
+  // block of token `tok` of the call (-1: past the call, a skipped slot or an
+  // unmapped block); block ids are below 2^31 (num_blocks * num_kv_heads is)
+  auto block_of = [&](int64_t tok) -> int {
+    if (tok < 0 || tok >= T) return -1;
+    const int64_t slot = slots[tok];
+    return (slot >= 0 && slot / BS < NB) ? static_cast<int>(slot / BS) : -1;
+  };
+  const int ba = block_of(t0 + lane);
+  const int bb = BS <= 64 ? block_of(t0 + 64 + lane) : -1;
+  const int bp = block_of(t0 - 1);  // the token before the window
+  // token j continues a run when it and token j - 1 lie in one block
+  int pa = __shfl_up(ba, 1, 64), pb = __shfl_up(bb, 1, 64);
+  const int last_a = __shfl(ba, 63, 64);
+  if (lane == 0) {
+    pa = bp;
+    pb = last_a;
   }
-  unsigned long long starts = __ballot(start);
+  const bool start = ba >= 0 && pa != ba;
+  uint64_t starts = __ballot(start);
+  const uint64_t ca = __ballot(ba >= 0 && pa == ba), cb = __ballot(bb >= 0 && pb == bb);
   while (starts != 0ull) {  // uniform
     const int i = __ffsll(static_cast<long long>(starts)) - 1;
     starts &= starts - 1ull;
     const int64_t t = t0 + i;
     const int64_t slot = slots[t];
     const int64_t blk = slot / BS;
-    int r = 1;
-    while (t + r < T) {
-      const int64_t nx = slots[t + r];
-      if (nx < 0 || nx / BS != blk) break;
-      ++r;
+    int r;
+    if (BS <= 64) {
+      // 1 + the continuation bits after i: through the window, then into the next
+      const uint64_t x = i < 63 ? (ca >> (i + 1)) : 0ull;
+      const int n1 = __builtin_ctzll(~x);
+      const int n2 = (n1 == 63 - i) ? (~cb == 0ull ? 64 : __builtin_ctzll(~cb)) : 0;
+      r = 1 + n1 + n2;
+    } else {
+      r = 1;
+      while (t + r < T) {
+        const int64_t nx = slots[t + r];
+        if (nx < 0 || nx / BS != blk) break;
+        ++r;
+      }
     }
     const int first = static_cast<int>(slot % BS);
+    // a whole block at offsets 0..15 in token order (a slot mapping may order a
+    // block's tokens otherwise: then the general path)
+    if (BS == 16 && first == 0 && r == 16 && __all(slots[t + (lane & 15)] == slot + (lane & 15)) &&
+        fp8_append_block16<D>(kc, vc, ks, vs, key, kst, ksh, val, vst, vsh, t, blk, h, H))
+      continue;
     fp8_append_run_vec<D, false>(kc, ks, key, kst, ksh, slots, t, r, blk, first, h, H, BS);
     fp8_append_run_vec<D, true>(vc, vs, val, vst, vsh, slots, t, r, blk, first, h, H, BS);
   }
