@@ -7,18 +7,18 @@
 // Memory pipeline. The partition is streamed in 32-token steps (36 KB). Each
 // step is copied HBM -> LDS by global_load_lds_dwordx4 (lane i of a wave
 // instruction lands at LDS base + 16 i), with no register staging, into one
-// of three LDS buffers; two steps are in flight while the third is computed.
-// A wave waits only for its own copies of the step about to be used
-// (s_waitcnt vmcnt(n)) and a barrier publishes everyone's. The buffers are
-// distinct __shared__ objects indexed statically, so the compiler can prove
-// that reading one never aliases the copies still landing in the others.
+// of four LDS buffers: the copy waves keep two steps in flight while the QK
+// and PV waves compute on the other two. A copy wave waits only for its own
+// copies of the step about to be used (s_waitcnt vmcnt(n)) and a barrier
+// publishes everyone's. The copies and their waits are inline asm, so the
+// compiler's own wait insertion never drains the copies in flight.
 //
 // LDS layout of a step: row t (token), 72 chunks of 16 bytes; chunk c of row
 // t sits at slot c ^ swz(t), so the QK reads (16 rows, same chunk) run
 // without bank conflicts.
 //
-// Per step, with waves w = 0..NW-1 and HPB 16-head blocks per wave:
-//   QK  S^T[32 tok, heads of w] = C[32 tok, 576] . Q^T   (mfma_f32_16x16x32_bf16,
+// Per step (the wave roles are described at the kernel):
+//   QK  S^T[32 tok, 16 heads of w] = C[32 tok, 576] . Q^T   (mfma_f32_16x16x32_bf16,
 //       A = latent rows from LDS, B = Q^T resident in registers)
 //       online softmax per head; P^T (bf16) and the rescale factors -> LDS.
 //   PV  O^T[d-slice of w, all heads] += C^T[d, 32 tok] . P^T
@@ -169,17 +169,23 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const float *__restrict_
 }
 
 // A workgroup owns HW = 16 NQ of the H = HW * HG heads of one (sequence,
-// partition) and runs 2 NQ waves in two roles, one of each per SIMD:
+// partition) and runs 3 NQ waves in three roles, one of each per SIMD:
 //   QK waves (w < NQ):  Q^T of heads 16 w .. 16 w + 15 in registers; compute
 //       S for step s + 1, the online softmax, and write P^T and the rescale
 //       factors of that step to LDS.
-//   PV waves (w >= NQ): the output accumulators of d-slice (w - NQ) for all
-//       HW heads; issue the LDS copies, rescale, and accumulate O for step s.
+//   PV waves (NQ <= w < 2 NQ): the output accumulators of d-slice (w - NQ)
+//       for all HW heads; rescale and accumulate O for step s.
+//   copy waves (w >= 2 NQ): issue the LDS copies of step s + 3 and wait for
+//       those of step s + 2.
 // One barrier per step hands step s + 1's probabilities from the QK waves to
 // the PV waves, which consume them one step later -- so on every SIMD the QK
 // wave's softmax and bookkeeping overlap the PV wave's MFMAs and the two
-// waves' MFMAs interleave. Four 36 KB step buffers: the PV waves read step s,
-// the QK waves step s + 1, and steps s + 2 and s + 3 are in flight.
+// waves' MFMAs interleave. An LDS-DMA copy stalls the wave that issues it
+// until the memory pipeline takes it (about 1,250 cycles per 36 KB step at
+// full load, measured), so the copies have waves of their own, which hold
+// no accumulators and stall without holding back an MFMA. Four 36 KB step
+// buffers: the PV waves read step s, the QK waves step s + 1, and steps
+// s + 2 and s + 3 are in flight.
 //
 // The 1-D grid is laid out for the dispatcher, which deals workgroup i to XCD
 // i mod 8: work item k = (sequence, partition) goes to XCD k mod 8, and its HG
@@ -187,7 +193,7 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const float *__restrict_
 // XCD and dispatched back to back, so the second read of each latent tile is
 // served by that XCD's L2.
 template <int NQ>
-__global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
+__global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     uint16_t *__restrict__ lat, const uint16_t *__restrict__ qn, int64_t qn_sb, int64_t qn_sh,
     const uint16_t *__restrict__ qp, int64_t qp_sb, int64_t qp_sh, uint16_t *__restrict__ out,
     float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
@@ -220,8 +226,8 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
   const int part = __builtin_amdgcn_readfirstlane(item % max_parts);
   const int hbase = HW * (wg_r >> 3);  // first head of this workgroup
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const bool is_qk = wave < NQ;
-  const int role_w = is_qk ? wave : wave - NQ;  // QK: head block; PV: d-slice
+  const int role = wave / NQ;          // 0: QK, 1: PV, 2: copies
+  const int role_w = wave - NQ * role;  // QK: head block; PV: d-slice; copies: instruction set
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int t_begin = part * P_tok;
   const int blk_first = __builtin_amdgcn_readfirstlane(t_begin / BS);
@@ -239,7 +245,7 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
   const int nparts = L > 0 ? (L + P_tok - 1) / P_tok : 0;
   if (nparts == 0) {
     if (part == 0) {
-      for (int e = threadIdx.x; e < HW * R / 8; e += 128 * NQ)
+      for (int e = threadIdx.x; e < HW * R / 8; e += 192 * NQ)
         reinterpret_cast<u32x4 *>(out + (static_cast<int64_t>(b) * H + hbase) * R)[e] = u32x4{0u, 0u, 0u, 0u};
     }
     return;
@@ -254,12 +260,12 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
   const int s_new = (L - 1 - t_begin) / STEP;
   const int tn = (L - 1 - t_begin) - STEP * s_new;
 
-  // The two roles run separate loops with the same barrier sequence
+  // The three roles run separate loops with the same barrier sequence
   // (prologue, one per step, epilogue), so each role's registers are live
   // only in its own branch.
-  if (!is_qk) {
-    // ------------------------------------------------------------ PV role
-    // Copies: PV wave p issues the step's wave-instructions p, p + NQ, ...;
+  if (role == 2) {
+    // ---------------------------------------------------------- copy role
+    // Copies: copy wave p issues the step's wave-instructions p, p + NQ, ...;
     // for each, the token of the step and its byte offset t * ROWB + chunk,
     // packed as (t << 16) | offset (offsets are < 2^16), fixed for every step.
     uint32_t cp_tok_off[NIW];
@@ -311,6 +317,39 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
       }
     };
 
+    const int n_pre = nsteps < 3 ? nsteps : 3;  // steps copied before the loop
+    for (int s = 0; s < n_pre; ++s) issue(s);
+    // Step 0 landed once at most the later prologue copies are pending (the
+    // counter holds 63: with one copy wave, wait for step 1 as well).
+    if (n_pre == 3)
+      wait_vmcnt<(2 * NIW < 64 ? 2 * NIW : NIW)>();
+    else if (n_pre == 2)
+      wait_vmcnt<NIW>();
+    else
+      wait_vmcnt<0>();
+    barrier_lds();  // step 0 visible to the QK waves
+    if (nsteps > 1) {
+      if (n_pre == 3)  // step 1 landed
+        wait_vmcnt<NIW>();
+      else
+        wait_vmcnt<0>();
+    }
+    for (int s = 0; s < nsteps; ++s) {
+      barrier_lds();  // step s + 1 landed, buffer of step s - 1 free
+      const bool more = s + 3 < nsteps;
+      if (more) issue(s + 3);
+      // Step s + 2 must have landed before the next barrier.
+      if (more)
+        wait_vmcnt<NIW>();
+      else
+        wait_vmcnt<0>();
+    }
+    __syncthreads();  // the epilogue barrier of the other roles
+    return;
+  }
+
+  if (role == 1) {
+    // ------------------------------------------------------------ PV role
     // Operand offsets. The transposed read of source lane (g, k, q) covers
     // row 4 g + k, elements d0 + 4 q .. + 3 of this wave's d-slice.
     const int tk = (lane >> 2) & 3, tq = lane & 3;
@@ -366,33 +405,10 @@ __global__ __launch_bounds__(128 * NQ, 1) void decode_mla_kernel(
       }
     };
 
-    const int n_pre = nsteps < 3 ? nsteps : 3;  // steps copied before the loop
-    for (int s = 0; s < n_pre; ++s) issue(s);
-    // Step 0 landed once at most the later prologue copies are pending (the
-    // counter holds 63: with one PV wave, wait for step 1 as well).
-    if (n_pre == 3)
-      wait_vmcnt<(2 * NIW < 64 ? 2 * NIW : NIW)>();
-    else if (n_pre == 2)
-      wait_vmcnt<NIW>();
-    else
-      wait_vmcnt<0>();
-    barrier_lds();  // step 0 visible to the QK waves
-    if (nsteps > 1) {
-      if (n_pre == 3)  // step 1 landed
-        wait_vmcnt<NIW>();
-      else
-        wait_vmcnt<0>();
-    }
+    barrier_lds();  // step 0 landed
     for (int s = 0; s < nsteps; ++s) {
-      barrier_lds();  // P(s) written, step s + 1 landed, buffer of step s - 1 free
-      const bool more = s + 3 < nsteps;
-      if (more) issue(s + 3);
+      barrier_lds();  // P(s) written, step s + 1 landed
       pv_step(s);
-      // Step s + 2 must have landed before the next barrier.
-      if (more)
-        wait_vmcnt<NIW>();
-      else
-        wait_vmcnt<0>();
     }
     __syncthreads();  // the QK waves' denominators and maxima are in LDS
 
@@ -542,7 +558,7 @@ static int mla_partition_blocks(int p, int BS) {
 }
 
 // Head groups per (sequence, partition): 128 heads run as two workgroups of
-// 64 (4 waves, one per SIMD), every smaller count as one.
+// 64 (12 waves, three per SIMD), every smaller count as one.
 static int mla_head_groups(int num_heads) { return num_heads == 128 ? 2 : 1; }
 
 // Tokens per partition when the caller leaves it to the library: one
@@ -624,7 +640,7 @@ static int launch_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t 
   auto qpp = static_cast<const uint16_t *>(q_pe);
   auto oo = static_cast<uint16_t *>(out);
 #define WKV_MLA(NQv)                                                                                        \
-  decode_mla_kernel<NQv><<<grid, 128 * NQv, 0, s>>>(lat, qn, qn_stride_b, qn_stride_h, qpp, qp_stride_b,          \
+  decode_mla_kernel<NQv><<<grid, 192 * NQv, 0, s>>>(lat, qn, qn_stride_b, qn_stride_h, qpp, qp_stride_b,          \
                                                     qp_stride_h, oo, part_o, part_ml, block_table, bt_stride,      \
                                                     max_blocks_per_seq, max_seq, seq_lens, BS, cache->num_blocks, \
                                                     scale_log2, partition_size, max_parts, num_heads, batch, ap)
