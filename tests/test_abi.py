@@ -142,7 +142,8 @@ def test_workspace_sizes():
     assert lib.wkv_decode_workspace_size(64, 32, 128, 4096, 256) == 64 * 32 * 16 * 130 * 4
     assert lib.wkv_decode_workspace_size(64, 32, 128, 4096, 0) == 64 * 32 * 32 * 130 * 4
     assert lib.wkv_decode_workspace_size(-1, 32, 128, 4096, 0) == -1
-    assert lib.wkv_mla_workspace_size(32, 128, 512, 4096, 512) == 32 * 128 * 8 * 514 * 4
+    # MLA: 32 seqs x 128 heads x 8 partitions x (bf16 partial of 512 + fp32 maximum and sum)
+    assert lib.wkv_mla_workspace_size(32, 128, 512, 4096, 512) == 32 * 128 * 8 * (512 * 2 + 8)
 
 
 @host_only

@@ -135,9 +135,11 @@ struct MlaAppend {
 };
 
 // Log-sum-exp merge of the per-partition partials of one (sequence, head):
-// 128 lanes per head, four output elements (one 16-byte partial load per
-// partition) per lane, two heads per 256-thread workgroup.
-__global__ __launch_bounds__(256) void mla_merge_kernel(const float *__restrict__ part_o,
+// 128 lanes per head, four output elements (one 8-byte partial load per
+// partition) per lane, two heads per 256-thread workgroup. A partial is the
+// partition's normalised output o_p (bf16) with its maximum m_p and sum l_p:
+// out = sum_p 2^(m_p - M) l_p o_p / sum_p 2^(m_p - M) l_p.
+__global__ __launch_bounds__(256) void mla_merge_kernel(const uint16_t *__restrict__ part_o,
                                                         const float *__restrict__ part_ml, uint16_t *__restrict__ out,
                                                         const int32_t *__restrict__ seq_lens, int max_seq, int H,
                                                         int P_tok, int max_parts) {
@@ -155,11 +157,11 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const float *__restrict_
   floatx4 num = {0.f, 0.f, 0.f, 0.f};
   float den = 0.f;
   for (int p = 0; p < nparts; ++p) {
-    const float w = exp2f(part_ml[2 * (row0 + p)] - m_use);
-    den += w * part_ml[2 * (row0 + p) + 1];
-    const floatx4 o = *reinterpret_cast<const floatx4 *>(part_o + (row0 + p) * R + d);
+    const float wl = exp2f(part_ml[2 * (row0 + p)] - m_use) * part_ml[2 * (row0 + p) + 1];
+    den += wl;
+    const u32x2 o = *reinterpret_cast<const u32x2 *>(part_o + (row0 + p) * R + d);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) num[i] += w * o[i];
+    for (int i = 0; i < 4; ++i) num[i] += wl * __uint_as_float((o[i >> 1] >> (16 * (i & 1))) << 16);
   }
   const float inv = den > 0.f ? 1.f / den : 0.f;
   u32x2 v;
@@ -196,7 +198,7 @@ template <int NQ>
 __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     uint16_t *__restrict__ lat, const uint16_t *__restrict__ qn, int64_t qn_sb, int64_t qn_sh,
     const uint16_t *__restrict__ qp, int64_t qp_sb, int64_t qp_sh, uint16_t *__restrict__ out,
-    float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
+    uint16_t *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
     int Mb, int max_seq, const int32_t *__restrict__ seq_lens, int BS, int64_t NB, float scale_log2, int P_tok,
     int max_parts, int H, int batch, MlaAppend ap) {
   using namespace mla;
@@ -412,24 +414,20 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     }
     __syncthreads();  // the QK waves' denominators and maxima are in LDS
 
-    // ---- epilogue: normalised output, or this partition's partials.
+    // ---- epilogue: the normalised output, or this partition's (bf16) partial.
 #pragma unroll
     for (int c = 0; c < NHB; ++c) {
       const int hl = 16 * c + col, h = hbase + hl;
       const float lh = lsum_s[hl];
+      const float inv = lh > 0.f ? 1.f / lh : 0.f;
+      uint16_t *dst = nparts == 1 ? out + (static_cast<int64_t>(b) * H + h) * R
+                                  : part_o + ((static_cast<int64_t>(b) * H + h) * max_parts + part) * R;
 #pragma unroll
       for (int a = 0; a < NDT; ++a) {
-        const int d0 = role_w * DSL + 16 * a + 4 * grp;
-        if (nparts == 1) {
-          const float inv = lh > 0.f ? 1.f / lh : 0.f;
-          u32x2 w;
-          w[0] = pack_bf16x2(acc[a][c][0] * inv, acc[a][c][1] * inv);
-          w[1] = pack_bf16x2(acc[a][c][2] * inv, acc[a][c][3] * inv);
-          *reinterpret_cast<u32x2 *>(out + (static_cast<int64_t>(b) * H + h) * R + d0) = w;
-        } else {
-          const int64_t row = (static_cast<int64_t>(b) * H + h) * max_parts + part;
-          *reinterpret_cast<floatx4 *>(part_o + row * R + d0) = acc[a][c];
-        }
+        u32x2 w;
+        w[0] = pack_bf16x2(acc[a][c][0] * inv, acc[a][c][1] * inv);
+        w[1] = pack_bf16x2(acc[a][c][2] * inv, acc[a][c][3] * inv);
+        *reinterpret_cast<u32x2 *>(dst + role_w * DSL + 16 * a + 4 * grp) = w;
       }
       if (nparts > 1 && role_w == 0 && grp == 0) {
         const int64_t row = (static_cast<int64_t>(b) * H + h) * max_parts + part;
@@ -583,7 +581,8 @@ extern "C" int64_t wkv_mla_workspace_size(int32_t batch, int32_t num_heads, int3
   if (batch < 0 || num_heads <= 0 || kv_lora_rank <= 0 || max_seq_len < 0 || partition_size < 0) return -1;
   if (partition_size == 0) partition_size = mla::STEP;  // the smallest partition the library picks by itself
   const int64_t max_parts = (static_cast<int64_t>(max_seq_len) + partition_size - 1) / partition_size;
-  return static_cast<int64_t>(batch) * num_heads * (max_parts > 0 ? max_parts : 1) * (kv_lora_rank + 2) * 4;
+  // per (sequence, head, partition): the bf16 partial output, then its maximum and sum (fp32)
+  return static_cast<int64_t>(batch) * num_heads * (max_parts > 0 ? max_parts : 1) * (kv_lora_rank * 2 + 8);
 }
 
 namespace wkv {
@@ -626,8 +625,9 @@ static int launch_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t 
   if (max_parts > 1)
     WKV_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= need,
                   "workspace too small: need %lld bytes, got %lld", (long long)need, (long long)workspace_bytes);
-  float *part_o = static_cast<float *>(workspace);
-  float *part_ml = part_o ? part_o + static_cast<int64_t>(batch) * num_heads * max_parts * 512 : nullptr;
+  uint16_t *part_o = static_cast<uint16_t *>(workspace);
+  float *part_ml = part_o ? reinterpret_cast<float *>(part_o + static_cast<int64_t>(batch) * num_heads * max_parts * 512)
+                          : nullptr;
   const float scale_log2 = scale * 1.4426950408889634f;
   auto s = static_cast<hipStream_t>(stream);
   const int HG = mla_head_groups(num_heads);
