@@ -212,7 +212,7 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
 
   __shared__ __attribute__((aligned(16))) uint8_t buf[NBUF][STEPB];
   __shared__ __attribute__((aligned(16))) uint8_t pt[2][NHB * 1024];  // P^T per step parity, [hb][g][col][8 bf16]
-  __shared__ float corr_s[2][HW];                                     // rescale factors per step parity, [col][hb]
+  __shared__ __attribute__((aligned(16))) float corr_s[2][HW];        // rescale factors per step parity, [col][hb]
   __shared__ float lsum_s[HW];
   __shared__ float mrun_s[HW];
 
@@ -367,9 +367,6 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     StepPos ppos{0, off_first};  // the next step to accumulate
 
     auto pv_step = [&](int s) __attribute__((always_inline)) {
-      const StepSrc src = step_src(lat, ppos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
-      advance(ppos, BS);
-      if (!src.any) return;
       const uint8_t *cur = &buf[s & (NBUF - 1)][0];
       const uint8_t *pts = &pt[s & 1][0];
       typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s4;
@@ -380,23 +377,42 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)(cur + o + HALF));
         return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       };
-      bf16x8 pb[NHB];
-#pragma unroll
-      for (int c = 0; c < NHB; ++c) {
-        const float cr = corr_s[s & 1][col * NHB + c];  // rescale factor of head 16 c + col
-        pb[c] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(pts + c * 1024 + pt_w));
-        if (__builtin_amdgcn_ballot_w64(cr != 1.f)) {
-#pragma unroll
-          for (int a = 0; a < NDT; ++a)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[a][c][i] *= cr;
-        }
-      }
-      // A-operand reads run PVPF d-tiles ahead of the MFMAs.
+      // Every read the step starts with is issued before the first wait: the
+      // first A operands, P^T and the rescale factors (one read). A-operand
+      // reads then run PVPF d-tiles ahead of the MFMAs.
       constexpr int PVPF = 2;
       bf16x8 va[PVPF + 1];
 #pragma unroll
       for (int a = 0; a < PVPF && a < NDT; ++a) va[a] = load_va(a);
+      bf16x8 pb[NHB];
+#pragma unroll
+      for (int c = 0; c < NHB; ++c)
+        pb[c] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(pts + c * 1024 + pt_w));
+      float cr[NHB];  // rescale factor of head 16 c + col
+      if constexpr (NHB == 4) {
+        const floatx4 v = *reinterpret_cast<const floatx4 *>(&corr_s[s & 1][col * NHB]);
+#pragma unroll
+        for (int c = 0; c < NHB; ++c) cr[c] = v[c];
+      } else {
+#pragma unroll
+        for (int c = 0; c < NHB; ++c) cr[c] = corr_s[s & 1][col * NHB + c];
+      }
+      // The step's bookkeeping runs while those reads are in flight (a skipped
+      // step leaves them unused).
+      const StepSrc src = step_src(lat, ppos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
+      advance(ppos, BS);
+      if (!src.any) return;
+      bool moved = false;
+#pragma unroll
+      for (int c = 0; c < NHB; ++c) moved |= cr[c] != 1.f;
+      if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+        for (int a = 0; a < NDT; ++a)
+#pragma unroll
+          for (int c = 0; c < NHB; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[a][c][i] *= cr[c];
+      }
 #pragma unroll
       for (int a = 0; a < NDT; ++a) {
         if (a + PVPF < NDT) va[(a + PVPF) % (PVPF + 1)] = load_va(a + PVPF);
@@ -473,9 +489,6 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
   const int pt_w = ((grp * 16) + col) * 16;
 
   auto qk_step = [&](int s) __attribute__((always_inline)) {
-    const StepSrc src = step_src(lat, qpos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
-    advance(qpos, BS);
-    if (!src.any) return;
     const uint8_t *cur = &buf[s & (NBUF - 1)][0];
     // S^T for the 32 tokens; A-operand reads run QKPF k-steps ahead (a ring
     // of register slots; the scheduling fence keeps them there).
@@ -492,6 +505,10 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     };
 #pragma unroll
     for (int j = 0; j < QKPF; ++j) qk_load(j);
+    // The step's bookkeeping runs while the first reads are in flight.
+    const StepSrc src = step_src(lat, qpos, t_begin + STEP * s, t_end, BS, my_blk, NBi);
+    advance(qpos, BS);
+    if (!src.any) return;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       if (j + QKPF < NJ) qk_load(j + QKPF);
