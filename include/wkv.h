@@ -191,6 +191,31 @@ int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64
                                 int32_t partition_size, void *workspace, int64_t workspace_bytes,
                                 const int32_t *seq_order, void *stream);
 
+/* The two GQA decode calls with a per-head attention sink: sinks[h] (fp32,
+ * device memory, one per query head, natural-log units like the scaled
+ * scores; -inf = none) is one more logit in head h's softmax whose value
+ * vector is zero, so o[b, h] = sum_t e^(s_t) v_t / (sum_t e^(s_t) + e^(sinks[h]))
+ * and a zero-length sequence still gives zeros. Otherwise the arguments and
+ * behaviour of wkv_paged_decode_gqa / wkv_append_paged_decode_gqa. Replaces
+ * the learned sink of the reference's sparse attention
+ * (wavelet/trainer/models/deepseek_v4/attention.py:89-95: torch.cat of the
+ * scores with the sink, softmax, sink column dropped; the sinks parameter of
+ * attention.py:703), which its decode backend must honour. */
+int wkv_paged_decode_gqa_sinks(const wkv_cache_t *cache, const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                               void *out, int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
+                               int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                               int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
+                               int64_t workspace_bytes, const int32_t *seq_order, const float *sinks, void *stream);
+
+int wkv_append_paged_decode_gqa_sinks(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                      int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                      int64_t value_stride_h, const int64_t *slot_mapping, const void *q,
+                                      int64_t q_stride_b, int64_t q_stride_h, void *out, int32_t num_q_heads,
+                                      const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                      const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                                      int32_t partition_size, void *workspace, int64_t workspace_bytes,
+                                      const int32_t *seq_order, const float *sinks, void *stream);
+
 /* Allocation-free variant of wkv_append_paged_decode_gqa, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): the same arguments and result

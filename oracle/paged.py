@@ -198,13 +198,22 @@ def dequant_gathered(codes: np.ndarray, scales: np.ndarray, block_table, seq_len
 # ---------------------------------------------------------------------------
 # Attention
 
-def _softmax_rows(s: np.ndarray) -> np.ndarray:
+def _softmax_rows(s: np.ndarray, sink=None) -> np.ndarray:
+    """Row softmax; with ``sink`` (one logit per row) each row's softmax also
+    holds that logit, whose probability is dropped: the learned zero-value sink
+    of wavelet/trainer/models/deepseek_v4/attention.py:89-95 (scores
+    concatenated with the sink, softmax, last column removed)."""
     m = s.max(axis=-1, keepdims=True)
+    if sink is None:
+        e = np.exp(s - m)
+        return e / e.sum(axis=-1, keepdims=True)
+    sink = np.asarray(sink, dtype=s.dtype).reshape(-1, 1)
+    m = np.maximum(m, sink)
     e = np.exp(s - m)
-    return e / e.sum(axis=-1, keepdims=True)
+    return e / (e.sum(axis=-1, keepdims=True) + np.exp(sink - m))
 
 
-def decode_gqa(q, k_vals, v_vals, block_table, seq_lens, scale, *, p_bf16=False, dtype=np.float64):
+def decode_gqa(q, k_vals, v_vals, block_table, seq_lens, scale, *, p_bf16=False, dtype=np.float64, sinks=None):
     """GQA paged decode: ``o[i, h] = softmax(q[i,h] . K_i^T * scale) . V_i``.
 
     ``q`` is ``[B, Hq, D]`` values; ``k_vals``/``v_vals`` are logical
@@ -212,8 +221,10 @@ def decode_gqa(q, k_vals, v_vals, block_table, seq_lens, scale, *, p_bf16=False,
     Query head ``h`` reads KV head ``h // (Hq // Hkv)``. Scores and softmax in
     ``dtype`` (fp32 scores/softmax as at attention.py:89-93); with ``p_bf16``
     the probabilities are rounded to bf16 before PV, as attention.py:94-96 casts
-    them to the KV dtype (the reference bf16 path). A zero-length sequence
-    gives zeros. Returns ``[B, Hq, D]`` in ``dtype``.
+    them to the KV dtype (the reference bf16 path). ``sinks`` (``[Hq]``,
+    natural-log logits, ``-inf`` = none) adds each head's zero-value sink
+    logit to its softmax (``_softmax_rows``). A zero-length sequence gives
+    zeros. Returns ``[B, Hq, D]`` in ``dtype``.
     """
     q = np.asarray(q)
     b, hq, d = q.shape
@@ -230,7 +241,8 @@ def decode_gqa(q, k_vals, v_vals, block_table, seq_lens, scale, *, p_bf16=False,
         vv = v_vals[blk, pos % bs].astype(dtype)
         for h in range(hkv):
             qh = q[i, h * g : (h + 1) * g].astype(dtype)  # [G, D]
-            p = _softmax_rows((qh @ kk[:, h].T) * dtype(scale))
+            sink = None if sinks is None else np.asarray(sinks, dtype=dtype)[h * g : (h + 1) * g]
+            p = _softmax_rows((qh @ kk[:, h].T) * dtype(scale), sink)
             if p_bf16:
                 p = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(dtype)
             out[i, h * g : (h + 1) * g] = p @ vv[:, h]

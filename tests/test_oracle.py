@@ -361,6 +361,85 @@ def test_decode_gqa_reference_ignore_slot_known_answer():
     np.testing.assert_allclose(out, expected, rtol=1e-12, atol=1e-12)
 
 
+def sink_case():
+    """The reference's known answer with its sink passed as a sink.
+
+    tests/test_deepseek_attention.py:100-118: query [0.5, -0.25], one real key
+    = value [2, -1], scaling 0.5, a zero-logit zero-value sink (the ``sinks``
+    parameter of attention.py:89-95), an ignored slot. Output =
+    sigmoid(0.625) * [2, -1]. Here the ignored slot is every slot past the
+    one-token context, poisoned with NaN; head_dim is padded to 64 with zeros.
+    """
+    nb, bs, h, d = 2, 16, 1, 64
+    kc = np.full((nb, bs, h, d), np.nan, np.float32)
+    vc = np.full((nb, bs, h, d), np.nan, np.float32)
+    kc[1, 0], vc[1, 0] = 0.0, 0.0
+    kc[1, 0, 0, :2] = [2.0, -1.0]
+    vc[1, 0, 0, :2] = [2.0, -1.0]
+    q = np.zeros((1, 1, d), np.float32)
+    q[0, 0, :2] = [0.5, -0.25]
+    bt = np.array([[1]], np.int32)
+    lens = np.array([1], np.int32)
+    expected = np.zeros((1, 1, d))
+    expected[0, 0, :2] = (1.0 / (1.0 + math.exp(-0.625))) * np.array([2.0, -1.0])
+    return kc, vc, q, bt, lens, 0.5, np.zeros(1, np.float32), expected
+
+
+def test_decode_gqa_sink_reference_known_answer():
+    kc, vc, q, bt, lens, scale, sinks, expected = sink_case()
+    out = paged.decode_gqa(q, kc, vc, bt, lens, scale, sinks=sinks)
+    np.testing.assert_allclose(out, expected, rtol=1e-12, atol=1e-12)
+
+
+def test_decode_gqa_sink_equals_a_zero_value_token():
+    """A sink s_h is the same as one more token per sequence whose key scores
+    exactly s_h against the query (k = q s_h / (scale |q|^2)) and whose value is
+    zero; checked with one query head per KV head so that key can be built."""
+    rng = np.random.default_rng(7)
+    b, h, d, bs, scale = 5, 3, 64, 16, 0.125
+    lens = np.array([0, 1, 17, 40, 33], np.int32)
+    nblk = (lens.max() + 1 + bs - 1) // bs
+    bt = np.arange(b * nblk, dtype=np.int32).reshape(b, nblk)
+    kc = rng.standard_normal((b * nblk, bs, h, d))
+    vc = rng.standard_normal((b * nblk, bs, h, d))
+    q = rng.standard_normal((b, h, d))
+    sinks = np.array([0.7, -2.5, 4.0])
+    out = paged.decode_gqa(q, kc, vc, bt, lens, scale, sinks=sinks)
+    k2, v2 = kc.copy(), vc.copy()
+    for i in range(b):
+        pos = lens[i]
+        blk, off = bt[i, pos // bs], pos % bs
+        for hh in range(h):
+            k2[blk, off, hh] = q[i, hh] * (sinks[hh] / (scale * float(q[i, hh] @ q[i, hh])))
+            v2[blk, off, hh] = 0.0
+    ref = paged.decode_gqa(q, k2, v2, bt, lens + 1, scale)
+    np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+    assert np.all(out[0] == 0.0)  # no context: the sink takes everything
+
+
+def test_decode_gqa_sink_closed_forms():
+    """-inf sinks change nothing; n identical keys and values under a sink s
+    give v * n / (n + e^(s - c)), c the common score."""
+    rng = np.random.default_rng(8)
+    b, hq, hkv, d, bs, scale = 3, 4, 2, 64, 16, 0.25
+    lens = np.array([5, 16, 31], np.int32)
+    bt = np.arange(b * 2, dtype=np.int32).reshape(b, 2)
+    kc = rng.standard_normal((b * 2, bs, hkv, d))
+    vc = rng.standard_normal((b * 2, bs, hkv, d))
+    q = rng.standard_normal((b, hq, d))
+    none = paged.decode_gqa(q, kc, vc, bt, lens, scale)
+    np.testing.assert_array_equal(paged.decode_gqa(q, kc, vc, bt, lens, scale, sinks=np.full(hq, -np.inf)), none)
+    kc[:] = kc[0, 0]
+    vc[:] = vc[0, 0]
+    sinks = np.array([-1.0, 0.0, 2.0, 5.0])
+    out = paged.decode_gqa(q, kc, vc, bt, lens, scale, sinks=sinks)
+    for i in range(b):
+        for h in range(hq):
+            c = float(q[i, h] @ kc[0, 0, h // 2]) * scale
+            n = float(lens[i])
+            np.testing.assert_allclose(out[i, h], vc[0, 0, h // 2] * n / (n + math.exp(sinks[h] - c)), rtol=1e-12)
+
+
 def test_decode_mla_matches_explicit_non_absorbed_attention():
     """Absorbed MLA == per-head attention with K = W_UK c + rope, V = W_UV c (then W_UV folded out)."""
     rank, rope, hn, heads, dv = 32, 8, 16, 4, 16

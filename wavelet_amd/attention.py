@@ -107,6 +107,7 @@ def paged_decode_gqa(
     new_value: torch.Tensor | None = None,
     slot_mapping: torch.Tensor | None = None,
     seq_order: torch.Tensor | None = None,
+    sinks: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One decode step of GQA attention: ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` bf16.
 
@@ -118,7 +119,10 @@ def paged_decode_gqa(
     attention reads it -- the same result as ``cache.append`` then this call.
     ``seq_order`` (int32 ``[B]``, a permutation of ``0..B-1``, e.g. from
     ``decode_order``) sets the order in which sequences are dispatched; the
-    result is the same, bit for bit, in any order.
+    result is the same, bit for bit, in any order. ``sinks`` (fp32 ``[Hq]``,
+    natural-log logits, ``-inf`` = none) adds one zero-value logit per query
+    head to its softmax: the learned sink of the reference's sparse attention
+    (wavelet/trainer/models/deepseek_v4/attention.py:89-95).
     """
     if not isinstance(cache, PagedKVCache):
         raise ValueError("cache must be a PagedKVCache")
@@ -139,6 +143,11 @@ def paged_decode_gqa(
         if new_key.shape[0] != batch or new_value.shape[0] != batch:
             raise ValueError(f"new_key/new_value must hold one token per sequence ({batch})")
         slot_mapping = _slots(slot_mapping, batch, dev)
+    if sinks is not None:
+        if (not isinstance(sinks, torch.Tensor) or sinks.dtype != torch.float32 or tuple(sinks.shape) != (hq,)
+                or sinks.device != dev):
+            raise ValueError(f"sinks must be a float32 [{hq}] tensor on {dev}")
+        sinks = sinks.contiguous()
     if out is None:
         out = torch.empty((batch, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, hq, cache.head_dim) or not out.is_contiguous():
@@ -153,14 +162,16 @@ def paged_decode_gqa(
     ws = _workspace(dev, need)
     tail = (q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), hq, block_table.data_ptr(),
             block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl, float(scale),
-            int(partition_size), ws.data_ptr(), ws.numel(),
-            _order(seq_order, batch, dev), _stream(dev))
+            int(partition_size), ws.data_ptr(), ws.numel(), _order(seq_order, batch, dev))
+    tail = tail + ((sinks.data_ptr(),) if sinks is not None else ()) + (_stream(dev),)
+    desc = ctypes.byref(cache.descriptor())
     if fused:
-        rc = lib.wkv_append_paged_decode_gqa(
-            ctypes.byref(cache.descriptor()), new_key.data_ptr(), new_key.stride(0), new_key.stride(1),
-            new_value.data_ptr(), new_value.stride(0), new_value.stride(1), slot_mapping.data_ptr(), *tail)
+        fn = lib.wkv_append_paged_decode_gqa_sinks if sinks is not None else lib.wkv_append_paged_decode_gqa
+        rc = fn(desc, new_key.data_ptr(), new_key.stride(0), new_key.stride(1), new_value.data_ptr(),
+                new_value.stride(0), new_value.stride(1), slot_mapping.data_ptr(), *tail)
     else:
-        rc = lib.wkv_paged_decode_gqa(ctypes.byref(cache.descriptor()), *tail)
+        fn = lib.wkv_paged_decode_gqa_sinks if sinks is not None else lib.wkv_paged_decode_gqa
+        rc = fn(desc, *tail)
     _lib.check(rc, "paged_decode_gqa")
     return out
 

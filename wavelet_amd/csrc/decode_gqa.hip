@@ -32,6 +32,14 @@ __device__ __forceinline__ int balanced_partition(int n, int W, int P_tok, int u
   return __builtin_amdgcn_readfirstlane(p);
 }
 
+// Weight of query head hq's attention sink in a softmax denominator whose
+// terms are 2^(s - m_use) (log2 domain): the sink is an extra logit with a
+// zero value vector (wavelet/trainer/models/deepseek_v4/attention.py:89-95),
+// given in natural-log units like the scaled scores. No sinks: 0.
+__device__ __forceinline__ float sink_weight(const float *sinks, int hq, float m_use) {
+  return sinks != nullptr ? exp2f(sinks[hq] * 1.4426950408889634f - m_use) : 0.f;
+}
+
 // Grid: (chunk, KV head, sequence or dispatch rank); W waves per workgroup, wave w of chunk c
 // owns partition c*W + w of P_tok tokens. The waves of a workgroup merge
 // their partials through LDS; a context longer than one chunk leaves one
@@ -42,7 +50,8 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ out,
     float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
     int Mb, int max_seq, const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ order, int Hq, int Hkv,
-    int G, int BS, int64_t NB, float scale_log2, int P_tok, int max_chunks, StepAppend ap) {
+    int G, int BS, int64_t NB, float scale_log2, int P_tok, int max_chunks, StepAppend ap,
+    const float *__restrict__ sinks) {
   const int chunk = blockIdx.x, kvh = blockIdx.y;
   // The wave index is uniform across the wave; saying so keeps everything
   // derived from it (partition, block ids, buffer resources) in scalar registers.
@@ -167,7 +176,8 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     if (col >= G) return;
     const int hq = kvh * G + col;
     if (nchunks == 1) {
-      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float den = l + sink_weight(sinks, hq, st.m == -INFINITY ? 0.f : st.m);
+      const float inv = den > 0.f ? 1.f / den : 0.f;
       uint16_t *op = out + (static_cast<int64_t>(b) * Hq + hq) * D;
 #pragma unroll
       for (int n = 0; n < D / 16; ++n) {
@@ -215,6 +225,7 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
       }
       const int hq = kvh * G + h;
       if (final_out) {
+        den += sink_weight(sinks, hq, m_use);
         out[(static_cast<int64_t>(b) * Hq + hq) * D + d] =
             static_cast<uint16_t>(f32_to_bf16_bits(den > 0.f ? num / den : 0.f));
       } else {
@@ -239,7 +250,7 @@ template <int D, typename Slots>
 __global__ __launch_bounds__(256) void merge_partials_kernel(const float *__restrict__ part_o,
                                                              const float *__restrict__ part_ml,
                                                              uint16_t *__restrict__ out, int rows, int Hq, int slots,
-                                                             Slots sl) {
+                                                             Slots sl, const float *__restrict__ sinks) {
   constexpr int SPEC = 4;    // slots whose outputs are loaded speculatively
   constexpr int E = D / 64;  // d values per lane
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -273,7 +284,7 @@ __global__ __launch_bounds__(256) void merge_partials_kernel(const float *__rest
   float den = used(lane) && lane < slots ? exp2f(m_l - m_use) * l_l : 0.f;
   for (int p = lane + 64; p < slots; p += 64)
     if (used(p)) den += exp2f(part_ml[2 * (base + p)] - m_use) * part_ml[2 * (base + p) + 1];
-  den = wave_sum(den);
+  den = wave_sum(den) + sink_weight(sinks, row % Hq, m_use);
   float acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
@@ -668,7 +679,7 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
                          int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
                          float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
                          const StepAppend *ap, const int32_t *seq_order, void *stream,
-                         bool static_scratch = false) {
+                         bool static_scratch = false, const float *sinks = nullptr) {
   int rc = check_cache(cache, -1);
   if (rc) return rc;
   WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
@@ -727,7 +738,8 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
                                                              block_table, bt_stride, max_blocks_per_seq,       \
                                                              max_seq, seq_lens, seq_order,                     \
                                                              num_q_heads, Hkv, G, BS, cache->num_blocks,       \
-                                                             scale_log2, partition_size, max_chunks, apv)
+                                                             scale_log2, partition_size, max_chunks, apv,      \
+                                                             sinks)
 #define WKV_DECODE_W(Dv, F8, AP)   \
   do {                             \
     if (W == 1)                    \
@@ -753,9 +765,11 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
     const int rows = batch * num_q_heads;
     const PlainSlots ps{seq_lens, max_seq, partition_size * W};
     if (D == 128)
-      merge_partials_kernel<128><<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads, max_chunks, ps);
+      merge_partials_kernel<128>
+          <<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads, max_chunks, ps, sinks);
     else
-      merge_partials_kernel<64><<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads, max_chunks, ps);
+      merge_partials_kernel<64>
+          <<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads, max_chunks, ps, sinks);
     WKV_CHECK_LAUNCH("paged decode merge");
   }
   return WKV_OK;
@@ -880,10 +894,10 @@ static int launch_grouped(const wkv_cache_t *cache, const StepAppend *ap, const 
   const GroupSlots gs{gg, seq_lens, max_seq, batch, BS, kGroupW * P};
   if (D == 128)
     merge_partials_kernel<128><<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads,
-                                                              static_cast<int>(slots), gs);
+                                                              static_cast<int>(slots), gs, nullptr);
   else
     merge_partials_kernel<64><<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads,
-                                                             static_cast<int>(slots), gs);
+                                                             static_cast<int>(slots), gs, nullptr);
   WKV_CHECK_LAUNCH("grouped paged decode merge");
   return WKV_OK;
 }
@@ -951,6 +965,18 @@ extern "C" int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int
                        workspace_bytes, nullptr, seq_order, stream);
 }
 
+extern "C" int wkv_paged_decode_gqa_sinks(const wkv_cache_t *cache, const void *q, int64_t q_stride_b,
+                                          int64_t q_stride_h, void *out, int32_t num_q_heads,
+                                          const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                          const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                                          int32_t partition_size, void *workspace, int64_t workspace_bytes,
+                                          const int32_t *seq_order, const float *sinks, void *stream) {
+  WKV_CHECK_ARG(sinks != nullptr && reinterpret_cast<uintptr_t>(sinks) % 4 == 0, "sinks must be non-NULL fp32");
+  return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
+                       max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
+                       workspace_bytes, nullptr, seq_order, stream, false, sinks);
+}
+
 extern "C" int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
                                            int64_t key_stride_h, const void *value, int64_t value_stride_t,
                                            int64_t value_stride_h, const int64_t *slot_mapping, const void *q,
@@ -972,6 +998,30 @@ extern "C" int wkv_append_paged_decode_gqa(const wkv_cache_t *cache, const void 
   return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
                        max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
                        workspace_bytes, &ap, seq_order, stream);
+}
+
+extern "C" int wkv_append_paged_decode_gqa_sinks(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                                 int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                                 int64_t value_stride_h, const int64_t *slot_mapping, const void *q,
+                                                 int64_t q_stride_b, int64_t q_stride_h, void *out,
+                                                 int32_t num_q_heads, const int32_t *block_table, int64_t bt_stride,
+                                                 int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                                                 int32_t max_seq_len, float scale, int32_t partition_size,
+                                                 void *workspace, int64_t workspace_bytes, const int32_t *seq_order,
+                                                 const float *sinks, void *stream) {
+  WKV_CHECK_ARG(sinks != nullptr && reinterpret_cast<uintptr_t>(sinks) % 4 == 0, "sinks must be non-NULL fp32");
+  WKV_CHECK_ARG(key && value && aligned16(key) && aligned16(value), "key/value must be non-NULL and 16-byte aligned");
+  WKV_CHECK_ARG(key_stride_t >= 0 && key_stride_h >= 0 && value_stride_t >= 0 && value_stride_h >= 0 &&
+                    (key_stride_t | key_stride_h | value_stride_t | value_stride_h) % 8 == 0,
+                "key/value strides must be non-negative multiples of 8");
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  if (cache != nullptr && cache->kv_dtype == WKV_KV_FP8_E4M3)
+    WKV_CHECK_ARG(cache->k_scale && cache->v_scale, "fp8 cache needs k_scale and v_scale");
+  const StepAppend ap{static_cast<const uint16_t *>(key), key_stride_t, key_stride_h,
+                      static_cast<const uint16_t *>(value), value_stride_t, value_stride_h, slot_mapping};
+  return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
+                       max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
+                       workspace_bytes, &ap, seq_order, stream, false, sinks);
 }
 
 // ---------------------------------------------------------------------------
