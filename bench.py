@@ -60,6 +60,9 @@ def parse() -> argparse.Namespace:
                          "instead of decoding every member separately")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device to device (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--phase-clocks", action="store_true",
+                    help="deepseek-v3-mla only: run the attention with the profiling library "
+                         "(python -m wavelet_amd.build --phase-clocks) and print its per-phase cycle counts")
     return ap.parse_args()
 
 
@@ -433,10 +436,71 @@ def workload(args, torch, dev) -> dict:
             "logical_kv_bytes": int(L.sum()) * 2 * HKV * D * kv_bytes}
 
 
+def phase_clocks(args) -> int:
+    """Per-phase shader-clock cycles of the MLA decode kernel, from the profiling
+    build of the library (libwkv_phase.so, compiled with WKV_PHASE_CLOCKS): one
+    warm pass over the layers, then one layer's launch, then the medians over
+    its workgroups of each phase's cycles per step."""
+    import ctypes
+
+    import wavelet_amd._lib as L
+    from wavelet_amd.build import PHASE_LIB
+
+    if args.workload != "deepseek-v3-mla":
+        print("--phase-clocks applies to the deepseek-v3-mla workload", file=sys.stderr)
+        return 2
+    if not PHASE_LIB.exists():
+        print(f"{PHASE_LIB} is missing: python -m wavelet_amd.build --phase-clocks", file=sys.stderr)
+        return 2
+    L.LIB_PATH = PHASE_LIB
+    import torch
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    wl = workload(args, torch, dev)
+    step = wl["step"]
+    for _ in range(3):
+        for layer in range(args.layers):
+            step.attend(layer)
+    torch.cuda.synchronize()
+    step.attend(0)
+    torch.cuda.synchronize()
+    lib = L.load()
+    lib.wkv_mla_phase_clocks.restype = ctypes.c_int
+    lib.wkv_mla_phase_clocks.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    n = 1024 * 16
+    buf = np.zeros(n, np.uint64)
+    if lib.wkv_mla_phase_clocks(buf.ctypes.data, n) != 0:
+        print("reading the phase clocks failed", file=sys.stderr)
+        return 1
+    r = buf.reshape(-1, 16).astype(np.float64)
+    r = r[r[:, 2] > 0]
+    steps = r[:, 2]
+    med = lambda i: round(float(np.median(r[:, i] / steps)), 1)
+    res = {
+        "metric": "MLA decode phase cycles (s_memtime, median workgroup)", "workload": wl["desc"],
+        "workgroups": int(len(r)), "steps": int(np.median(steps)),
+        "cycles_per_workgroup": round(float(np.median(r[:, 0])), 0),
+        "wall_us_per_workgroup": round(float(np.median(r[:, 1])) / 100.0, 2),
+        "shader_clock_ghz": round(float(np.median(r[:, 0] / (r[:, 1] * 10.0))), 3),
+        "launch_wall_us": round(float(r[:, 13].max() - r[:, 12].min()) / 100.0, 2),
+        "per_step": {
+            "copy": {"barrier": med(3), "issue": med(4), "wait": med(5)},
+            "pv": {"barrier": med(8), "operand_reads": med(9), "mfma": med(10)},
+            "qk": {"barrier": med(11), "mfma": med(14), "softmax": med(15)},
+        },
+        "prologue": {"copy": round(float(np.median(r[:, 7])), 0), "pv": round(float(np.median(r[:, 6])), 0)},
+    }
+    print(json.dumps(res))
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.calibrate_copy:
         return calibrate_copy()
+    if args.phase_clocks:
+        return phase_clocks(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); run it with --gpus 1", file=sys.stderr)
         return 2

@@ -21,6 +21,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libwkv.so"
+PHASE_LIB = PKG / "libwkv_phase.so"  # profiling build (build_phase_clocks)
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -120,6 +121,12 @@ def build(verbose: bool = False) -> Path:
     return _build(LIB, [], [], verbose)
 
 
+def build_phase_clocks(out: Path | None = None, verbose: bool = False) -> Path:
+    """The library with the MLA decode's per-phase cycle stamps (WKV_PHASE_CLOCKS;
+    read by `bench.py --phase-clocks`), at `out` (default PHASE_LIB). Profiling only."""
+    return _build(Path(out) if out is not None else PHASE_LIB, ["-DWKV_PHASE_CLOCKS"], [], verbose)
+
+
 def build_sanitized(out: Path, verbose: bool = False) -> Path:
     """The same library with AddressSanitizer and UndefinedBehaviorSanitizer on its host code, at `out`."""
     return _build(Path(out), SANITIZE_COMPILE, SANITIZE_LINK, verbose)
@@ -138,4 +145,7 @@ def asan_runtime() -> Path | None:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    if "--phase-clocks" in sys.argv[1:]:
+        print(build_phase_clocks(verbose=True))
+    else:
+        print(build(verbose=True))

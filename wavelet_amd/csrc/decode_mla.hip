@@ -123,6 +123,52 @@ __device__ __forceinline__ bool token_ok(const StepSrc &s, int t) {
 
 }  // namespace mla
 
+// Profiling builds only (-DWKV_PHASE_CLOCKS, wavelet_amd.build --phase-clocks):
+// every workgroup below kPhaseWgs sums the shader-clock cycles (s_memtime) of
+// its step phases per role into 16 slots of g_mla_phase, read back with
+// wkv_mla_phase_clocks (include/wkv_profile.h):
+//   0 cycles, 1 wall ticks (100 MHz), 2 steps, 12 / 13 wall start / end;
+//   copy waves: 3 barrier, 4 issue, 5 wait, 7 prologue;
+//   PV waves:   8 barrier, 9 operand reads before the first MFMA, 10 MFMAs, 6 prologue;
+//   QK waves:   11 barrier, 14 MFMAs (with their operand reads), 15 softmax.
+// s_memtime is a scalar-memory read; waiting for it also waits for the wave's
+// LDS reads in flight, so the stamps shift work across phase borders slightly.
+constexpr int kPhaseWgs = 1024;
+#ifdef WKV_PHASE_CLOCKS
+__device__ unsigned long long g_mla_phase[kPhaseWgs * 16];
+#define WKV_PHASE_INIT                                                                                 \
+  const unsigned long long ph_t0 = __builtin_amdgcn_s_memtime(), ph_r0 = __builtin_amdgcn_s_memrealtime(); \
+  unsigned long long ph_tp = ph_t0, ph_c[4] = {0, 0, 0, 0};
+#define WKV_PHASE(i)                                         \
+  {                                                          \
+    const unsigned long long t_ = __builtin_amdgcn_s_memtime(); \
+    ph_c[i] += t_ - ph_tp;                                   \
+    ph_tp = t_;                                              \
+  }
+#define WKV_PHASE_STORE(s0, s1, s2, s3)                                            \
+  if (lane == 0 && role_w == 0 && blockIdx.x < kPhaseWgs) {                        \
+    unsigned long long *r_ = g_mla_phase + 16 * blockIdx.x;                        \
+    const int sl_[4] = {s0, s1, s2, s3};                                           \
+    for (int i_ = 0; i_ < 4; ++i_)                                                 \
+      if (sl_[i_] >= 0) r_[sl_[i_]] = ph_c[i_];                                    \
+  }
+#define WKV_PHASE_TOTAL(n)                                                                             \
+  if (lane == 0 && role_w == 0 && blockIdx.x < kPhaseWgs) {                                            \
+    unsigned long long *r_ = g_mla_phase + 16 * blockIdx.x;                                            \
+    const unsigned long long r1_ = __builtin_amdgcn_s_memrealtime();                                   \
+    r_[0] = __builtin_amdgcn_s_memtime() - ph_t0;                                                      \
+    r_[1] = r1_ - ph_r0;                                                                               \
+    r_[2] = static_cast<unsigned long long>(n);                                                        \
+    r_[12] = ph_r0;                                                                                    \
+    r_[13] = r1_;                                                                                      \
+  }
+#else
+#define WKV_PHASE_INIT
+#define WKV_PHASE(i)
+#define WKV_PHASE_STORE(s0, s1, s2, s3)
+#define WKV_PHASE_TOTAL(n)
+#endif
+
 // The appended token of a fused append + decode step: row b of kv_c / k_pe
 // belongs to sequence b (its position seq_lens[b] - 1) and goes to slot
 // slots[b] (-1 = none). kvc == nullptr: attention only.
@@ -219,6 +265,7 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
   // The decode divides by runtime values, which the compiler does on the
   // vector unit; readfirstlane returns the (uniform) results to scalar
   // registers so everything derived from them stays scalar.
+  WKV_PHASE_INIT
   const int NBi = static_cast<int>(NB);  // the host bounds num_blocks to int32
   const int HG = H / HW;
   const int wg_r = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x % (8 * HG)));
@@ -336,16 +383,21 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
       else
         wait_vmcnt<0>();
     }
+    WKV_PHASE(3)
     for (int s = 0; s < nsteps; ++s) {
       barrier_lds();  // step s + 1 landed, buffer of step s - 1 free
+      WKV_PHASE(0)
       const bool more = s + 3 < nsteps;
       if (more) issue(s + 3);
+      WKV_PHASE(1)
       // Step s + 2 must have landed before the next barrier.
       if (more)
         wait_vmcnt<NIW>();
       else
         wait_vmcnt<0>();
+      WKV_PHASE(2)
     }
+    WKV_PHASE_STORE(3, 4, 5, 7)
     __syncthreads();  // the epilogue barrier of the other roles
     return;
   }
@@ -413,6 +465,7 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[a][c][i] *= cr[c];
       }
+      WKV_PHASE(1)
 #pragma unroll
       for (int a = 0; a < NDT; ++a) {
         if (a + PVPF < NDT) va[(a + PVPF) % (PVPF + 1)] = load_va(a + PVPF);
@@ -421,13 +474,18 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
         for (int c = 0; c < NHB; ++c)
           acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[a % (PVPF + 1)], pb[c], acc[a][c], 0, 0, 0);
       }
+      WKV_PHASE(2)
     };
 
+    WKV_PHASE(3)
     barrier_lds();  // step 0 landed
     for (int s = 0; s < nsteps; ++s) {
       barrier_lds();  // P(s) written, step s + 1 landed
+      WKV_PHASE(0)
       pv_step(s);
     }
+    WKV_PHASE_STORE(8, 9, 10, 6)
+    WKV_PHASE_TOTAL(nsteps)
     __syncthreads();  // the QK waves' denominators and maxima are in LDS
 
     // ---- epilogue: the normalised output, or this partition's (bf16) partial.
@@ -517,6 +575,7 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
       for (int tt = 0; tt < 2; ++tt)
         sc[j & 1][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ra[j % (QKPF + 1)][tt], qop[j], sc[j & 1][tt], 0, 0, 0);
     }
+    WKV_PHASE(1)
     // Online softmax; lane (col, grp) holds tokens 4 grp + i and 16 + 4 grp + i.
     float sv[8];
 #pragma unroll
@@ -546,14 +605,17 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     for (int i = 0; i < 4; ++i) pbv[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
     *reinterpret_cast<u32x4 *>(&pt[s & 1][role_w * 1024 + pt_w]) = pbv;
     if (grp == 0) corr_s[s & 1][col * NHB + role_w] = cr;
+    WKV_PHASE(2)
   };
 
   barrier_lds();  // step 0 landed
   qk_step(0);
   for (int s = 0; s < nsteps; ++s) {
     barrier_lds();  // step s + 1 landed; the PV waves are done with P(s - 1)
+    WKV_PHASE(0)
     if (s + 1 < nsteps) qk_step(s + 1);
   }
+  WKV_PHASE_STORE(11, 14, 15, -1)
   {
     float l = l_run + __shfl_xor(l_run, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -592,6 +654,14 @@ static int choose_mla_partition(int batch, int num_heads, int max_seq_len, int B
 }  // namespace wkv
 
 using namespace wkv;
+
+#ifdef WKV_PHASE_CLOCKS
+extern "C" int wkv_mla_phase_clocks(unsigned long long *dst, int n) {
+  if (dst == nullptr || n < 0 || n > kPhaseWgs * 16) return WKV_ERR_INVALID;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_mla_phase), static_cast<size_t>(n) * 8) == hipSuccess ? WKV_OK
+                                                                                                   : WKV_ERR_LAUNCH;
+}
+#endif
 
 extern "C" int64_t wkv_mla_workspace_size(int32_t batch, int32_t num_heads, int32_t kv_lora_rank,
                                           int32_t max_seq_len, int32_t partition_size) {
