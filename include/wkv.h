@@ -290,6 +290,18 @@ int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_t key_strid
                     int32_t max_blocks_per_seq, int32_t batch, int32_t max_query_len, int32_t max_seq_len,
                     float scale, void *stream);
 
+/* wkv_prefill_gqa with per-head attention sinks (sinks as for
+ * wkv_paged_decode_gqa_sinks: one zero-value logit per query head, fp32,
+ * natural-log units, -inf = none), the sinks of the reference's sparse
+ * attention (wavelet/trainer/models/deepseek_v4/attention.py:89-95). */
+int wkv_prefill_gqa_sinks(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
+                          const void *value, int64_t value_stride_t, int64_t value_stride_h,
+                          const int64_t *slot_mapping, int64_t num_tokens, const void *q, int64_t q_stride_t,
+                          int64_t q_stride_h, void *out, int64_t out_stride_t, int64_t out_stride_h,
+                          int32_t num_q_heads, const int32_t *cu_seqlens_q, const int32_t *seq_lens,
+                          const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq, int32_t batch,
+                          int32_t max_query_len, int32_t max_seq_len, float scale, const float *sinks, void *stream);
+
 /* Token sampler: the step after decode, producing what the engine records per
  * generated token -- the token, its processed logprob and the sampling mask
  * (llm.generate with logprobs_mode="processed_logprobs" and

@@ -249,7 +249,8 @@ def decode_gqa(q, k_vals, v_vals, block_table, seq_lens, scale, *, p_bf16=False,
     return out
 
 
-def prefill_gqa(q, k_vals, v_vals, block_table, seq_lens, cu_seqlens_q, scale, *, p_bf16=False, dtype=np.float64):
+def prefill_gqa(q, k_vals, v_vals, block_table, seq_lens, cu_seqlens_q, scale, *, p_bf16=False, dtype=np.float64,
+                sinks=None):
     """Varlen GQA prefill over a paged context (chunked prefill).
 
     Sequence ``i`` brings ``n_i = cu_seqlens_q[i+1] - cu_seqlens_q[i]`` new
@@ -259,7 +260,8 @@ def prefill_gqa(q, k_vals, v_vals, block_table, seq_lens, cu_seqlens_q, scale, *
     attends to positions ``0 .. L_i - n_i + j``: the causal mask of the
     engine's prompt step (``llm.generate``, wavelet/inference/engine.py:887)
     aligned to the end of the context, so an earlier chunk or a prefix-cache
-    hit is simply cached context. Scores and softmax as in ``decode_gqa``.
+    hit is simply cached context. Scores, softmax and ``sinks`` as in
+    ``decode_gqa``.
     Returns ``[T, Hq, D]`` in ``dtype``.
     """
     q = np.asarray(q)
@@ -282,7 +284,7 @@ def prefill_gqa(q, k_vals, v_vals, block_table, seq_lens, cu_seqlens_q, scale, *
             for hh in range(h * g, (h + 1) * g):
                 s = (q[q0:q1, hh].astype(dtype) @ kk[:, h].T) * dtype(scale)  # [n, L]
                 s = np.where(mask, s, -np.inf)
-                p = _softmax_rows(s)
+                p = _softmax_rows(s, None if sinks is None else np.full(n, sinks[hh], dtype=dtype))
                 if p_bf16:
                     p = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(dtype)
                 out[q0:q1, hh] = p @ vv[:, h]

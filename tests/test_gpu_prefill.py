@@ -62,14 +62,15 @@ def _case(cuda, name, hq, hkv, d, bs, qlens, lens, kv_dtype):
     return w, cache, (kc, vc, ks, vs), (kn, vn, q, nslots, cu)
 
 
-def _run_and_check(cuda, w, cache, host, new, what):
+def _run_and_check(cuda, w, cache, host, new, what, sinks=None):
     kc, vc, ks, vs = host
     kn, vn, q, nslots, cu = new
     bt = torch.from_numpy(w.block_tables).to(cuda)
     sl = torch.from_numpy(w.context_lens).to(cuda)
     out = prefill_gqa(to_dev_bits(q, BF16, cuda), cache, bt, sl, torch.from_numpy(cu).to(cuda), w.scale,
                       key=to_dev_bits(kn, BF16, cuda), value=to_dev_bits(vn, BF16, cuda),
-                      slot_mapping=torch.from_numpy(nslots).to(cuda))
+                      slot_mapping=torch.from_numpy(nslots).to(cuda),
+                      sinks=None if sinks is None else torch.from_numpy(sinks).to(cuda))
     if ks is not None:
         paged.append_fp8(kc, vc, ks, vs, kn, vn, nslots)
         kf = fp8.dequantize(paged.k_logical(kc).reshape(w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim),
@@ -83,7 +84,10 @@ def _run_and_check(cuda, w, cache, host, new, what):
     if ks is not None:
         np.testing.assert_array_equal(cache.k_scale.cpu().numpy(), ks)
         np.testing.assert_array_equal(cache.v_scale.cpu().numpy(), vs)
-    ref = paged.prefill_gqa(paged.bf16_to_f32(q), kf, vf, w.block_tables, w.context_lens, cu, w.scale)
+    ref = paged.prefill_gqa(paged.bf16_to_f32(q), kf, vf, w.block_tables, w.context_lens, cu, w.scale, sinks=sinks)
+    if sinks is not None:
+        plain = paged.prefill_gqa(paged.bf16_to_f32(q), kf, vf, w.block_tables, w.context_lens, cu, w.scale)
+        assert np.abs(ref - plain).max() > 0.1, f"{what}: the sinks must matter in this case"
     a, r = check_attention(paged.bf16_to_f32(bits_of(out)), ref, what)
     print(f"{what}: err abs {a:.2e} rel {r:.2e}")
     return out
@@ -100,6 +104,18 @@ def test_prefill_varlen_chunked(cuda, kv_dtype, hq, hkv, d, bs):
     name = f"pf{kv_dtype}{hq}{hkv}{d}{bs}"
     w, cache, host, new = _case(cuda, name, hq, hkv, d, bs, *MIX, kv_dtype)
     _run_and_check(cuda, w, cache, host, new, name)
+
+
+@pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
+@pytest.mark.parametrize("hq,hkv,d,bs", [(32, 8, 128, 16), (14, 2, 64, 16)])
+def test_prefill_with_attention_sinks(cuda, kv_dtype, hq, hkv, d, bs):
+    """Per-head sinks (a zero-value logit, wavelet/trainer/models/deepseek_v4/attention.py:89-95):
+    none (-inf), dominant, strongly negative and moderate ones, on the mixed varlen case."""
+    name = f"pfsink{kv_dtype}{hq}{hkv}{d}{bs}"
+    w, cache, host, new = _case(cuda, name, hq, hkv, d, bs, *MIX, kv_dtype)
+    sinks = (synth.normal(synth.stream_key(name, "sinks"), hq) * 2.0).astype(np.float32)
+    sinks[0], sinks[1], sinks[2] = -np.inf, 9.0, -6.0
+    _run_and_check(cuda, w, cache, host, new, name, sinks=sinks)
 
 
 def test_prefill_long_prompt_and_long_context_chunk(cuda):

@@ -519,3 +519,21 @@ def test_prefill_gqa_consistent_with_decode_and_closed_forms():
     j = 9
     dec_j = paged.decode_gqa(q[cu[2] + j][None], kv, vv, w.block_tables[2:3], np.array([44 + j + 1]), w.scale)
     np.testing.assert_allclose(got[cu[2] + j], dec_j[0], rtol=1e-12, atol=1e-13)
+
+
+def test_prefill_gqa_sinks_consistent_with_decode():
+    """With sinks, every new token equals the (independently pinned) decode with the
+    same sinks over the positions it sees; -inf sinks change nothing."""
+    qlens, lens = [7, 1, 20], [7, 50, 64]
+    w, kv, vv, cu, q = _prefill_case("pfs", 8, 2, 64, 16, qlens, lens)
+    sinks = np.array([-np.inf, 3.0, -1.0, 0.5, 8.0, -4.0, 1.5, 0.0])
+    got = paged.prefill_gqa(q, kv, vv, w.block_tables, w.context_lens, cu, w.scale, sinks=sinks)
+    for i in range(3):
+        for j in range(qlens[i]):
+            seen = lens[i] - qlens[i] + j + 1
+            dec = paged.decode_gqa(q[cu[i] + j][None], kv, vv, w.block_tables[i:i + 1], np.array([seen]), w.scale,
+                                   sinks=sinks)
+            np.testing.assert_allclose(got[cu[i] + j], dec[0], rtol=1e-12, atol=1e-13)
+    none = paged.prefill_gqa(q, kv, vv, w.block_tables, w.context_lens, cu, w.scale)
+    np.testing.assert_array_equal(
+        paged.prefill_gqa(q, kv, vv, w.block_tables, w.context_lens, cu, w.scale, sinks=np.full(8, -np.inf)), none)

@@ -62,6 +62,7 @@ _SIGNATURES = {
     "wkv_grouped_decode_workspace_size": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "wkv_paged_decode_gqa_grouped": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_void_p]),
     "wkv_prefill_gqa": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_float, c_void_p]),
+    "wkv_prefill_gqa_sinks": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_float, c_void_p, c_void_p]),
     "wkv_sample": (c_int, [c_void_p, c_int32, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "wkv_mla_workspace_size": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "wkv_paged_decode_mla": (c_int, [POINTER(WkvMlaCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p]),

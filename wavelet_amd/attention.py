@@ -143,11 +143,7 @@ def paged_decode_gqa(
         if new_key.shape[0] != batch or new_value.shape[0] != batch:
             raise ValueError(f"new_key/new_value must hold one token per sequence ({batch})")
         slot_mapping = _slots(slot_mapping, batch, dev)
-    if sinks is not None:
-        if (not isinstance(sinks, torch.Tensor) or sinks.dtype != torch.float32 or tuple(sinks.shape) != (hq,)
-                or sinks.device != dev):
-            raise ValueError(f"sinks must be a float32 [{hq}] tensor on {dev}")
-        sinks = sinks.contiguous()
+    sinks = _sinks(sinks, hq, dev)
     if out is None:
         out = torch.empty((batch, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, hq, cache.head_dim) or not out.is_contiguous():
@@ -263,6 +259,16 @@ def paged_decode_gqa_grouped(
     return out
 
 
+def _sinks(sinks: torch.Tensor | None, hq: int, dev: torch.device) -> torch.Tensor | None:
+    """Per-query-head attention sinks: None, or a contiguous float32 [Hq] device tensor."""
+    if sinks is None:
+        return None
+    if not isinstance(sinks, torch.Tensor) or sinks.dtype != torch.float32 or tuple(sinks.shape) != (hq,) \
+            or sinks.device != dev:
+        raise ValueError(f"sinks must be a float32 [{hq}] tensor on {dev}")
+    return sinks.contiguous()
+
+
 def prefill_gqa(
     q: torch.Tensor,
     cache: PagedKVCache,
@@ -277,6 +283,7 @@ def prefill_gqa(
     max_query_len: int | None = None,
     max_seq_len: int | None = None,
     out: torch.Tensor | None = None,
+    sinks: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Varlen (chunked) prefill: ``q [T, Hq, D]`` bf16 -> ``[T, Hq, D]`` bf16.
 
@@ -288,7 +295,7 @@ def prefill_gqa(
     the new tokens are appended first (``cache.append``) and attended from the
     cache -- the prompt step of ``llm.generate`` (wavelet/inference/
     engine.py:887). ``max_query_len`` / ``max_seq_len`` (host ints) avoid
-    device syncs when given.
+    device syncs when given. ``sinks`` as for ``paged_decode_gqa``.
     """
     if not isinstance(cache, PagedKVCache):
         raise ValueError("cache must be a PagedKVCache")
@@ -317,6 +324,7 @@ def prefill_gqa(
         out = torch.empty((tokens, hq, cache.head_dim), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (tokens, hq, cache.head_dim) or out.stride(2) != 1:
         raise ValueError("out must be a bfloat16 [T, Hq, D] tensor with a contiguous last dim")
+    sinks = _sinks(sinks, hq, dev)
     if max_query_len is None:
         max_query_len = int((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max().item()) if batch else 0
     msl = _max_len(seq_lens, max_seq_len)
@@ -326,10 +334,13 @@ def prefill_gqa(
                 slot_mapping.data_ptr(), tokens)
     else:
         head = (None, 0, 0, None, 0, 0, None, 0)
-    rc = lib.wkv_prefill_gqa(
-        ctypes.byref(cache.descriptor()), *head, q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(),
-        out.stride(0), out.stride(1), hq, cu_seqlens_q.data_ptr(), seq_lens.data_ptr(), block_table.data_ptr(),
-        block_table.stride(0), block_table.shape[1], batch, int(max_query_len), msl, float(scale), _stream(dev))
+    args = (ctypes.byref(cache.descriptor()), *head, q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(),
+            out.stride(0), out.stride(1), hq, cu_seqlens_q.data_ptr(), seq_lens.data_ptr(), block_table.data_ptr(),
+            block_table.stride(0), block_table.shape[1], batch, int(max_query_len), msl, float(scale))
+    if sinks is not None:
+        rc = lib.wkv_prefill_gqa_sinks(*args, sinks.data_ptr(), _stream(dev))
+    else:
+        rc = lib.wkv_prefill_gqa(*args, _stream(dev))
     _lib.check(rc, "prefill_gqa")
     return out
 

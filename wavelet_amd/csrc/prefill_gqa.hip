@@ -90,7 +90,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
     const float *__restrict__ vsc, const uint16_t *__restrict__ q, int64_t q_st,
     int64_t q_sh, uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
     const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
-    int Hkv, int G, int n_hg, int BS, int nb, float scale_log2, int n_qt, int n_items) {
+    int Hkv, int G, int n_hg, int BS, int nb, float scale_log2, int n_qt, int n_items,
+    const float *__restrict__ sinks) {
   using LT = LdsTile<D>;
   static_assert(kPrefillWaves == 4, "one tile per wave per 64-key step");
   static_assert(D % 64 == 0, "whole copies per lane");
@@ -429,6 +430,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
     const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
     l = __uint_as_float(x[0]) + __uint_as_float(x[1]);
   }
+  // An attention sink (a zero-value logit of head h, natural-log units) adds
+  // its weight against the row's reference maximum to the denominator.
+  if (sinks != nullptr) l += exp2f(sinks[h] * 1.4426950408889634f - m_ref);
   const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
@@ -445,13 +449,14 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
 
 using namespace wkv;
 
-extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
-                               const void *value, int64_t value_stride_t, int64_t value_stride_h,
-                               const int64_t *slot_mapping, int64_t num_tokens, const void *q, int64_t q_stride_t,
-                               int64_t q_stride_h, void *out, int64_t out_stride_t, int64_t out_stride_h,
-                               int32_t num_q_heads, const int32_t *cu_seqlens_q, const int32_t *seq_lens,
-                               const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
-                               int32_t batch, int32_t max_query_len, int32_t max_seq_len, float scale, void *stream) {
+static int launch_prefill(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
+                          const void *value, int64_t value_stride_t, int64_t value_stride_h,
+                          const int64_t *slot_mapping, int64_t num_tokens, const void *q, int64_t q_stride_t,
+                          int64_t q_stride_h, void *out, int64_t out_stride_t, int64_t out_stride_h,
+                          int32_t num_q_heads, const int32_t *cu_seqlens_q, const int32_t *seq_lens,
+                          const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq, int32_t batch,
+                          int32_t max_query_len, int32_t max_seq_len, float scale, const float *sinks,
+                          void *stream) {
   int rc = check_cache(cache, -1);
   if (rc) return rc;
   WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
@@ -502,7 +507,7 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
   prefill_gqa_kernel<Dv, F8><<<grid, 64 * kPrefillWaves, 0, s>>>(                                                \
       kc, vc, cache->k_scale, cache->v_scale, qq, q_stride_t, q_stride_h, oo, out_stride_t, out_stride_h,       \
       cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, max_seq, Hkv, G, n_hg, BS,           \
-      static_cast<int>(cache->num_blocks), scale_log2, n_qt, static_cast<int>(n_items))
+      static_cast<int>(cache->num_blocks), scale_log2, n_qt, static_cast<int>(n_items), sinks)
   if (D == 128) {
     if (fp8) WKV_PREFILL(128, true); else WKV_PREFILL(128, false);
   } else {
@@ -511,4 +516,33 @@ extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_
 #undef WKV_PREFILL
   WKV_CHECK_LAUNCH("paged prefill");
   return WKV_OK;
+}
+
+extern "C" int wkv_prefill_gqa(const wkv_cache_t *cache, const void *key, int64_t key_stride_t, int64_t key_stride_h,
+                               const void *value, int64_t value_stride_t, int64_t value_stride_h,
+                               const int64_t *slot_mapping, int64_t num_tokens, const void *q, int64_t q_stride_t,
+                               int64_t q_stride_h, void *out, int64_t out_stride_t, int64_t out_stride_h,
+                               int32_t num_q_heads, const int32_t *cu_seqlens_q, const int32_t *seq_lens,
+                               const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                               int32_t batch, int32_t max_query_len, int32_t max_seq_len, float scale, void *stream) {
+  return launch_prefill(cache, key, key_stride_t, key_stride_h, value, value_stride_t, value_stride_h, slot_mapping,
+                        num_tokens, q, q_stride_t, q_stride_h, out, out_stride_t, out_stride_h, num_q_heads,
+                        cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, batch, max_query_len,
+                        max_seq_len, scale, nullptr, stream);
+}
+
+extern "C" int wkv_prefill_gqa_sinks(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
+                                     int64_t key_stride_h, const void *value, int64_t value_stride_t,
+                                     int64_t value_stride_h, const int64_t *slot_mapping, int64_t num_tokens,
+                                     const void *q, int64_t q_stride_t, int64_t q_stride_h, void *out,
+                                     int64_t out_stride_t, int64_t out_stride_h, int32_t num_q_heads,
+                                     const int32_t *cu_seqlens_q, const int32_t *seq_lens,
+                                     const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                     int32_t batch, int32_t max_query_len, int32_t max_seq_len, float scale,
+                                     const float *sinks, void *stream) {
+  WKV_CHECK_ARG(sinks != nullptr && reinterpret_cast<uintptr_t>(sinks) % 4 == 0, "sinks must be non-NULL fp32");
+  return launch_prefill(cache, key, key_stride_t, key_stride_h, value, value_stride_t, value_stride_h, slot_mapping,
+                        num_tokens, q, q_stride_t, q_stride_h, out, out_stride_t, out_stride_h, num_q_heads,
+                        cu_seqlens_q, seq_lens, block_table, bt_stride, max_blocks_per_seq, batch, max_query_len,
+                        max_seq_len, scale, sinks, stream);
 }

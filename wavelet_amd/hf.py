@@ -147,7 +147,8 @@ class PagedCache(Cache):
         k._wavelet_paged = v._wavelet_paged = (self, layer)
         return k, v
 
-    def _attend(self, layer: int, query: torch.Tensor, scale: float) -> torch.Tensor:
+    def _attend(self, layer: int, query: torch.Tensor, scale: float,
+                sinks: torch.Tensor | None = None) -> torch.Tensor:
         k, v = self._pending.pop(layer)
         st = self._step
         b, hq, tokens, d = query.shape
@@ -158,11 +159,11 @@ class PagedCache(Cache):
         cache = self.pool.layers[layer]
         if tokens == 1:
             out = paged_decode_gqa(q, cache, st["block_table"], st["seq_lens"], scale, max_seq_len=st["max_seq_len"],
-                                   new_key=kk, new_value=vv, slot_mapping=st["slots"])
+                                   new_key=kk, new_value=vv, slot_mapping=st["slots"], sinks=sinks)
         else:
             out = prefill_gqa(q, cache, st["block_table"], st["seq_lens"], st["cu_seqlens_q"], scale, key=kk,
                               value=vv, slot_mapping=st["slots"], max_query_len=tokens,
-                              max_seq_len=st["max_seq_len"])
+                              max_seq_len=st["max_seq_len"], sinks=sinks)
         self.layers[layer].seen += tokens
         return out.view(b, tokens, hq, d)
 
@@ -171,7 +172,8 @@ def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: t
                             attention_mask: torch.Tensor | None, scaling: float | None = None, dropout: float = 0.0,
                             sliding_window: int | None = None, **kwargs):
     """``attention_interface`` for ``"wavelet_paged"``: ``query [B, Hq, T, D]`` and the key/value
-    that ``PagedCache.update`` returned -> ``([B, T, Hq, D], None)``."""
+    that ``PagedCache.update`` returned -> ``([B, T, Hq, D], None)``. ``s_aux`` (a model's per-head
+    attention sinks, as transformers passes them) becomes the kernels' ``sinks``."""
     tag = getattr(key, "_wavelet_paged", None)
     if tag is None:
         raise ValueError(f"{ATTN_IMPLEMENTATION!r} attention needs the key/value states PagedCache.update returned")
@@ -181,7 +183,9 @@ def paged_attention_forward(module: torch.nn.Module, query: torch.Tensor, key: t
         raise NotImplementedError("sliding-window attention is not supported on the paged path")
     cache, layer = tag
     scale = float(scaling) if scaling is not None else query.shape[-1] ** -0.5
-    return cache._attend(layer, query, scale), None
+    s_aux = kwargs.get("s_aux")
+    sinks = None if s_aux is None else s_aux.detach().to(device=query.device, dtype=torch.float32).contiguous()
+    return cache._attend(layer, query, scale, sinks), None
 
 
 def _no_mask(*args, **kwargs):
