@@ -193,6 +193,18 @@ def test_decode_mla_edge_lengths(cuda, heads):
         _mla_case(cuda, [0, 1, 17, 64, 65, 300, 1000], heads=heads, partition_size=p, tag=f"edge{heads}p{p}")
 
 
+@pytest.mark.parametrize("heads,partition", [(128, 64), (128, 0), (16, 32), (64, 160)])
+def test_decode_mla_batches_of_eight(cuda, heads, partition):
+    """Batches of 8 and 16 take the launch that puts every partition of a sequence on one XCD
+    (item k is sequence k mod 8 + 8 (k / 8 / P), partition k / 8 mod P): ragged lengths make the
+    partition counts differ between sequences, so a wrong sequence or partition index either
+    attends the wrong tokens or leaves a partial unwritten."""
+    lens = [0, 1, 17, 64, 65, 300, 1000, 4096]
+    _mla_case(cuda, lens, heads=heads, partition_size=partition, tag=f"b8h{heads}p{partition}")
+    _mla_case(cuda, lens[::-1] + [33, 2047, 96, 7, 640, 1, 128, 3000], heads=heads, partition_size=partition,
+              tag=f"b16h{heads}p{partition}")
+
+
 @pytest.mark.parametrize("bs,partition", [(16, 32), (16, 0), (64, 96), (32, 160), (128, 32)])
 def test_decode_mla_block_sizes_and_partitions(cuda, bs, partition):
     """32-token steps that straddle two blocks, partitions that start inside a block,
@@ -201,15 +213,17 @@ def test_decode_mla_block_sizes_and_partitions(cuda, bs, partition):
               tag=f"bs{bs}p{partition}")
 
 
-@pytest.mark.parametrize("heads,bs,partition", [(128, 64, 0), (16, 64, 96), (64, 16, 32), (32, 32, 0)])
-def test_fused_mla_append_decode_equals_append_then_decode(cuda, heads, bs, partition):
+@pytest.mark.parametrize("heads,bs,partition,nseq",
+                         [(128, 64, 0, 10), (16, 64, 96, 10), (64, 16, 32, 10), (32, 32, 0, 10), (128, 64, 64, 16)])
+def test_fused_mla_append_decode_equals_append_then_decode(cuda, heads, bs, partition, nseq):
     """One launch (latent append + MLA attention) leaves the cache bit-identical to
     wkv_mla_append and attends within tolerance of the separate path and of the oracle; the new
     token's slot and every unowned slot hold NaN before the step, so attending the new token from
-    the cache instead of its inputs, or reading past the context, shows up as NaN."""
+    the cache instead of its inputs, or reading past the context, shows up as NaN. A batch of 16
+    takes the launch that keeps the partitions of a sequence on one XCD."""
     R, P = 512, 64
-    lens = np.array([1, 2, 31, 32, 33, 64, 65, 300, 1024, 1025])
-    w = synth.make_decode_workload(f"fusedmla{heads}{bs}{partition}", batch=len(lens), num_kv_heads=1,
+    lens = np.array([1, 2, 31, 32, 33, 64, 65, 300, 1024, 1025, 3, 96, 97, 700, 2000, 129][:nseq])
+    w = synth.make_decode_workload(f"fusedmla{heads}{bs}{partition}n{nseq}", batch=len(lens), num_kv_heads=1,
                                    num_q_heads=heads, head_dim=R + P, block_size=bs, context_lens=lens,
                                    scale=1 / math.sqrt(192.0))
     own = _owned_mask(w)

@@ -236,17 +236,23 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const uint16_t *__restri
 // s + 2 and s + 3 are in flight.
 //
 // The 1-D grid is laid out for the dispatcher, which deals workgroup i to XCD
-// i mod 8: work item k = (sequence, partition) goes to XCD k mod 8, and its HG
-// head groups are workgroups 8 HG (k / 8) + 8 g + (k mod 8), i.e. on the same
-// XCD and dispatched back to back, so the second read of each latent tile is
-// served by that XCD's L2.
+// i mod 8: work item k goes to XCD k mod 8, and its HG head groups are
+// workgroups 8 HG (k / 8) + 8 g + (k mod 8), i.e. on the same XCD and
+// dispatched back to back, so the second read of each latent tile is served
+// by that XCD's L2. With a batch that is a multiple of 8 (seq_xcd), item k is
+// (sequence k mod 8 + 8 (k / 8 / P), partition k / 8 mod P) for P partitions
+// per sequence: every partition of a sequence sits on one XCD, so its q rows
+// are fetched from memory once rather than once per partition (measured:
+// 156 instead of 171 MB read per DeepSeek-V3 layer, same time); otherwise
+// item k is (sequence k / P, partition k mod P), which spreads the
+// partitions of a small batch over every XCD.
 template <int NQ>
 __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     uint16_t *__restrict__ lat, const uint16_t *__restrict__ qn, int64_t qn_sb, int64_t qn_sh,
     const uint16_t *__restrict__ qp, int64_t qp_sb, int64_t qp_sh, uint16_t *__restrict__ out,
     uint16_t *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
     int Mb, int max_seq, const int32_t *__restrict__ seq_lens, int BS, int64_t NB, float scale_log2, int P_tok,
-    int max_parts, int H, int batch, MlaAppend ap) {
+    int max_parts, int H, int batch, MlaAppend ap, int seq_xcd) {
   using namespace mla;
   constexpr int NHB = NQ;           // 16-head blocks of this workgroup
   constexpr int HW = 16 * NHB;      // heads of this workgroup
@@ -271,8 +277,8 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
   const int wg_r = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x % (8 * HG)));
   const int item = __builtin_amdgcn_readfirstlane(static_cast<int>(8 * (blockIdx.x / (8 * HG)) + (wg_r & 7)));
   if (static_cast<int64_t>(item) >= static_cast<int64_t>(batch) * max_parts) return;  // padding of the last group of 8
-  const int b = __builtin_amdgcn_readfirstlane(item / max_parts);
-  const int part = __builtin_amdgcn_readfirstlane(item % max_parts);
+  const int b = __builtin_amdgcn_readfirstlane(seq_xcd ? (item & 7) + 8 * ((item >> 3) / max_parts) : item / max_parts);
+  const int part = __builtin_amdgcn_readfirstlane(seq_xcd ? (item >> 3) % max_parts : item % max_parts);
   const int hbase = HW * (wg_r >> 3);  // first head of this workgroup
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int role = wave / NQ;          // 0: QK, 1: PV, 2: copies
@@ -730,7 +736,8 @@ static int launch_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t 
   decode_mla_kernel<NQv><<<grid, 192 * NQv, 0, s>>>(lat, qn, qn_stride_b, qn_stride_h, qpp, qp_stride_b,          \
                                                     qp_stride_h, oo, part_o, part_ml, block_table, bt_stride,      \
                                                     max_blocks_per_seq, max_seq, seq_lens, BS, cache->num_blocks, \
-                                                    scale_log2, partition_size, max_parts, num_heads, batch, ap)
+                                                    scale_log2, partition_size, max_parts, num_heads, batch, ap,  \
+                                                    batch % 8 == 0)
   switch (num_heads) {
     case 16: WKV_MLA(1); break;
     case 32: WKV_MLA(2); break;
