@@ -112,6 +112,7 @@ TRAFFIC_PROFILES = {
     ("qwen3-4b", "bf16"): "profiles/decode_gqa_qwen3_4b_pmc.md",
     ("qwen3-4b-var", "bf16"): "profiles/decode_gqa_qwen3_4b_var_pmc.md",
     ("qwen2.5-0.5b", "bf16"): "profiles/decode_gqa_qwen2_5_0_5b_pmc.md",
+    ("deepseek-v3-mla", "bf16"): "profiles/decode_mla_deepseek_v3.md",
 }
 
 
@@ -326,7 +327,8 @@ def workload(args, torch, dev) -> dict:
         append = B * (R + P) * 2 * 2 + B * 8
         flops = 2 * int(L.sum()) * H * (R + P + R)
         return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
-                "kernel": "decode_mla_kernel<4> x2 head groups (+ mla_merge_kernel)", "dtype": "bf16", "flops_per_layer": flops,
+                "kernel": "decode_mla_kernel<4> x2 head groups (+ mla_merge_kernel)", "dtype": "bf16", "kv_dtype": "bf16",
+                "flops_per_layer": flops,
                 "cache_bytes": cache_bytes,
                 "desc": f"DeepSeek-V3 MLA decode: {args.layers} layers x (latent append + absorbed attention), "
                         "128 heads, 512+64 latent, B=32, context 4096, block 64"}
@@ -628,7 +630,8 @@ def main() -> int:
                              "bytes": ceiling["bytes"], "workgroups": ceiling["workgroups"]},
     }
     traffic, source = measured_traffic(wl["name"], wl.get("kv_dtype", ""), kernel_name)
-    if traffic is not None and args.layers == ({"qwen3-4b": 36, "qwen3-4b-var": 36, "qwen2.5-0.5b": 24}
+    if traffic is not None and args.layers == ({"qwen3-4b": 36, "qwen3-4b-var": 36, "qwen2.5-0.5b": 24,
+                                                "deepseek-v3-mla": 8}
                                                .get(wl["name"], -1)) and args.partition == 0:
         rec["roofline"]["traffic"] = traffic
         rec["roofline"]["traffic_source"] = source
