@@ -225,7 +225,8 @@ def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0, grouped
     B, HQ, HKV, D, BS = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
     caches, qs, ks, vs, outs = [], [], [], [], []
     for _ in range(args.layers):
-        c = PagedKVCache(w.num_blocks, BS, HKV, D, kv_dtype=kv_dtype, device=dev)
+        # a workload whose groups share prompt blocks says so: the decode then keeps shared blocks cached
+        c = PagedKVCache(w.num_blocks, BS, HKV, D, kv_dtype=kv_dtype, device=dev, shared_blocks=w.group_size > 1)
         if kv_dtype == "bf16":
             c.k.normal_(generator=gen)
             c.v.normal_(generator=gen)

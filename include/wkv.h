@@ -64,7 +64,18 @@ typedef struct {
   int32_t num_kv_heads;
   int32_t head_dim;     /* 64 or 128 */
   int32_t kv_dtype;     /* wkv_kv_dtype_t */
+  int32_t flags;        /* WKV_CACHE_* bits, 0 = none */
+  int32_t reserved;     /* 0 */
 } wkv_cache_t;
+
+/* wkv_cache_t.flags: blocks of this cache are read by several sequences
+ * (prefix caching, GRPO groups sharing prompt blocks). The decode then reads
+ * K/V with the default cache policy, so a shared block read by one sequence
+ * stays cached for the next; without the flag it reads them as streamed,
+ * read-once data (non-temporal loads: 3-9% faster on unshared blocks,
+ * about 15% slower when blocks are shared). The group-aware decode sets its
+ * own policy per role and ignores the flag. */
+#define WKV_CACHE_SHARED_BLOCKS 1
 
 /* One layer of an MLA latent cache (bf16). */
 typedef struct {

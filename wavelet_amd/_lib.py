@@ -20,6 +20,10 @@ WKV_KV_BF16, WKV_KV_FP8_E4M3 = 0, 1
 WKV_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/wkv.h
 
 
+# wkv_cache_t.flags: several sequences read the same blocks (prefix caching)
+CACHE_SHARED_BLOCKS = 1
+
+
 class WkvCache(ctypes.Structure):
     _fields_ = [
         ("k", c_void_p),
@@ -31,6 +35,8 @@ class WkvCache(ctypes.Structure):
         ("num_kv_heads", c_int32),
         ("head_dim", c_int32),
         ("kv_dtype", c_int32),
+        ("flags", c_int32),
+        ("reserved", c_int32),
     ]
 
 

@@ -68,6 +68,7 @@ class PagedKVCache:
         head_dim: int,
         kv_dtype: str = "bf16",
         device: torch.device | str | None = None,
+        shared_blocks: bool = False,
     ) -> None:
         if kv_dtype not in KV_DTYPES:
             raise ValueError(f"kv_dtype must be one of {sorted(KV_DTYPES)} (got {kv_dtype!r})")
@@ -78,6 +79,8 @@ class PagedKVCache:
         if num_blocks <= 0 or num_kv_heads <= 0:
             raise ValueError("num_blocks and num_kv_heads must be positive")
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        # blocks read by several sequences (prefix caching): reads keep them cached
+        self.shared_blocks = bool(shared_blocks)
         self.num_blocks = int(num_blocks)
         self.block_size = int(block_size)
         self.num_kv_heads = int(num_kv_heads)
@@ -104,6 +107,7 @@ class PagedKVCache:
             num_kv_heads=self.num_kv_heads,
             head_dim=self.head_dim,
             kv_dtype=KV_DTYPES[self.kv_dtype],
+            flags=_lib.CACHE_SHARED_BLOCKS if self.shared_blocks else 0,
         )
 
     # -- sleep / wake (the engine's sleep(level=1) / wake_up(tags=["kv_cache"]),

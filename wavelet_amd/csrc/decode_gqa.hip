@@ -44,7 +44,9 @@ __device__ __forceinline__ float sink_weight(const float *sinks, int hq, float m
 // owns partition c*W + w of P_tok tokens. The waves of a workgroup merge
 // their partials through LDS; a context longer than one chunk leaves one
 // partial per chunk for merge_partials_kernel.
-template <int D, bool FP8, bool APPEND, int W>
+// STREAM: K/V tiles are read with the non-temporal policy (blocks read once);
+// a compile-time choice, as a runtime one costs the tile pipeline its schedule.
+template <int D, bool FP8, bool APPEND, int W, bool STREAM>
 __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ ks, float *__restrict__ vs,
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ out,
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     const int t_end = (t_begin + P_seq) < L ? (t_begin + P_seq) : L;
     const bool from_regs = APPEND && !FP8 && owns_new;  // last token comes from the inputs
     attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, from_regs ? L - 1 : t_end, kvh, Hkv, BS,
-                             NB, scale_log2, lane, col, grp);
+                             NB, scale_log2, lane, col, grp, STREAM);
     if constexpr (APPEND && !FP8) {
       if (owns_new) {
         Tile<D, FP8> tn;
@@ -400,6 +402,7 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_grouped_kernel(
     float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
     const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ order, int batch, int Hq, int Hkv, int G,
     int BS, int64_t NB, float scale_log2, int P_tok, StepAppend ap, GroupGeom gg) {
+  constexpr int stream = 1;  // the suffix role's tokens are private to their sequence: read once
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
   const int slots = gg.npp + gg.nsc;
@@ -439,8 +442,10 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_grouped_kernel(
     bf16x8 qop[D / 32];
     load_q<D, FP8>(qop, q + (valid ? b : b0) * q_sb + static_cast<int64_t>(kvh * G + (valid ? h : 0)) * q_sh,
                    valid, grp);
+    // the shared prompt blocks: the workgroup's four row-tile waves read each
+    // tile, so the loads keep the default cache policy
     attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, t_end, kvh, Hkv, BS, NB, scale_log2, lane,
-                             col, grp);
+                             col, grp, false);
     float l = st.l + __shfl_xor(st.l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     if (!valid) return;
@@ -510,7 +515,7 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_grouped_kernel(
     const int t_end = (t_begin + P_seq) < L ? (t_begin + P_seq) : L;
     const bool from_regs = APPEND && !FP8 && owns_new;
     attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, from_regs ? L - 1 : t_end, kvh, Hkv, BS,
-                             NB, scale_log2, lane, col, grp);
+                             NB, scale_log2, lane, col, grp, stream != 0);
     if constexpr (APPEND && !FP8) {
       if (owns_new) {
         Tile<D, FP8> tn;
@@ -732,14 +737,22 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
   const StepAppend none{nullptr, 0, 0, nullptr, 0, 0, nullptr};
   const StepAppend apv = ap ? *ap : none;
-#define WKV_DECODE(Dv, F8, AP, Wv)                                                                              \
-  decode_gqa_kernel<Dv, F8, AP, Wv><<<grid, 64 * Wv, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, qq,       \
-                                                             q_stride_b, q_stride_h, oo, part_o, part_ml,      \
-                                                             block_table, bt_stride, max_blocks_per_seq,       \
-                                                             max_seq, seq_lens, seq_order,                     \
-                                                             num_q_heads, Hkv, G, BS, cache->num_blocks,       \
-                                                             scale_log2, partition_size, max_chunks, apv,      \
-                                                             sinks)
+  const bool stream_reads = (cache->flags & WKV_CACHE_SHARED_BLOCKS) == 0;
+#define WKV_DECODE_S(Dv, F8, AP, Wv, ST)                                                                         \
+  decode_gqa_kernel<Dv, F8, AP, Wv, ST><<<grid, 64 * Wv, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, qq,     \
+                                                                 q_stride_b, q_stride_h, oo, part_o, part_ml,    \
+                                                                 block_table, bt_stride, max_blocks_per_seq,     \
+                                                                 max_seq, seq_lens, seq_order,                   \
+                                                                 num_q_heads, Hkv, G, BS, cache->num_blocks,     \
+                                                                 scale_log2, partition_size, max_chunks, apv,    \
+                                                                 sinks)
+#define WKV_DECODE(Dv, F8, AP, Wv)           \
+  do {                                       \
+    if (stream_reads)                        \
+      WKV_DECODE_S(Dv, F8, AP, Wv, true);    \
+    else                                     \
+      WKV_DECODE_S(Dv, F8, AP, Wv, false);   \
+  } while (0)
 #define WKV_DECODE_W(Dv, F8, AP)   \
   do {                             \
     if (W == 1)                    \
@@ -760,6 +773,7 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   }
 #undef WKV_DECODE_W
 #undef WKV_DECODE
+#undef WKV_DECODE_S
   WKV_CHECK_LAUNCH("paged decode");
   if (max_chunks > 1) {
     const int rows = batch * num_q_heads;

@@ -57,7 +57,9 @@ class KVPool:
             self.layers = [MLALatentCache(num_blocks, block_size, kv_lora_rank, rope_dim, device=device)
                            for _ in range(num_layers)]
         else:
-            self.layers = [PagedKVCache(num_blocks, block_size, num_kv_heads, head_dim, kv_dtype, device=device)
+            # with prefix caching, sequences share blocks: the decode keeps them cached between readers
+            self.layers = [PagedKVCache(num_blocks, block_size, num_kv_heads, head_dim, kv_dtype, device=device,
+                                        shared_blocks=enable_prefix_caching)
                            for _ in range(num_layers)]
         self.blocks = BlockManager(num_blocks, block_size, enable_prefix_caching=enable_prefix_caching,
                                    max_model_len=max_model_len)
