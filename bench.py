@@ -589,7 +589,8 @@ def main() -> int:
         from wavelet_amd import decode_plan
 
         _, waves, _ = decode_plan(w.batch, w.num_kv_heads, int(w.context_lens.max()), w.block_size, args.partition)
-        kernel_name = kernel_name.replace(",W>", f",{waves}>")
+        stream = "false" if w.group_size > 1 else "true"  # shared prompt blocks keep the default read policy
+        kernel_name = kernel_name.replace(",W>", f",{waves},{stream}>")
     rec = {
         "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx" if headline
         else wl.get("metric", f"decode-attn+KV-append GB/s & us/step, {wl['name']}"),
