@@ -58,6 +58,14 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--group-aware", action="store_true",
                     help="qwen2.5-7b-groups: the group-aware decode (each shared prompt block read once per group) "
                          "instead of decoding every member separately")
+    ap.add_argument("--via-pool", action="store_true",
+                    help="qwen3-4b / qwen3-4b-var: build the caches as the engine does -- a KVPool sized by "
+                         "KVPool.from_engine_config (gpu_memory_utilization 0.35), tables and slots from its block "
+                         "manager, each step's read policy from the manager's reference counts")
+    ap.add_argument("--graph", action="store_true",
+                    help="GQA decode workloads (not --group-aware): time replays of the whole step captured in one "
+                         "HIP graph (GraphDecodeStep, the allocation-free entry point) instead of eager launches; "
+                         "the eager step time is reported beside it")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device to device (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--phase-clocks", action="store_true",
@@ -215,18 +223,25 @@ def cpu_baseline(args, hq, hkv, d, bs, scale, per_layer_bytes) -> dict:
     }
 
 
+def gqa_cache(w, kv_dtype: str, dev):
+    """One layer's cache for a GQA workload, as every GQA workload builds it (the parity tests
+    of the benchmarked plans build theirs through this same call): a workload whose groups share
+    prompt blocks says so, and its decodes then keep shared blocks cached."""
+    from wavelet_amd import PagedKVCache
+
+    return PagedKVCache(w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim, kv_dtype=kv_dtype, device=dev,
+                        shared_blocks=w.group_size > 1)
+
+
 def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0, grouped: bool = False):
     """Per-layer caches (own memory per layer), step buffers and a DecodeStep plan
     (group-aware when `grouped`: the workload's groups share their prompt blocks)."""
-    from wavelet_amd import PagedKVCache
-
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
     B, HQ, HKV, D, BS = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
     caches, qs, ks, vs, outs = [], [], [], [], []
     for _ in range(args.layers):
-        # a workload whose groups share prompt blocks says so: the decode then keeps shared blocks cached
-        c = PagedKVCache(w.num_blocks, BS, HKV, D, kv_dtype=kv_dtype, device=dev, shared_blocks=w.group_size > 1)
+        c = gqa_cache(w, kv_dtype, dev)
         if kv_dtype == "bf16":
             c.k.normal_(generator=gen)
             c.v.normal_(generator=gen)
@@ -246,6 +261,77 @@ def _gqa_setup(torch, dev, args, w, kv_dtype: str, qkv_std: float = 1.0, grouped
         outs.append(torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev))
     step = gqa_plan(torch, dev, w, caches, qs, ks, vs, outs, args.partition, grouped)
     return step, caches[0].nbytes
+
+
+class _StepWithPolicy:
+    """A DecodeStep launched with one read policy for every step (the policy a serving loop
+    computes per step; fixed here because the benchmark's tables do not change)."""
+
+    grouped = False
+
+    def __init__(self, step, shared_blocks: bool) -> None:
+        self.step, self.shared_blocks = step, bool(shared_blocks)
+
+    def run(self) -> None:
+        self.step.run(shared_blocks=self.shared_blocks)
+
+    def step_layer(self, layer: int) -> None:
+        self.step.step_layer(layer, self.shared_blocks)
+
+    def attend(self, layer: int) -> None:
+        self.step.attend(layer, self.shared_blocks)
+
+    def append(self, layer: int) -> None:
+        self.step.append(layer)
+
+
+def _gqa_pool_setup(torch, dev, args, w, kv_dtype: str):
+    """The workload through the engine-facing surface: one KVPool sized by
+    KVPool.from_engine_config (the engine's default gpu_memory_utilization 0.35,
+    max_model_len = the longest context), every sequence's cached context allocated by the
+    pool's block manager (distinct salts: nothing shared), the step's slots from
+    KVPool.append_slots and its tables from the manager, and the read policy from the
+    manager's reference counts (KVPool.decode_shares_blocks). Returns the step, the cache
+    bytes per layer, and the workload with the manager's tables."""
+    import dataclasses
+
+    from wavelet_amd import KVPool
+    from wavelet_amd.plan import DecodeStep
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    B, HQ, HKV, D, BS = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
+    L = w.context_lens.astype(np.int64)
+    pool = KVPool.from_engine_config(num_layers=args.layers, num_kv_heads=HKV, head_dim=D, kv_dtype=kv_dtype,
+                                     block_size=BS, gpu_memory_utilization=0.35, max_model_len=int(L.max()),
+                                     device=dev)
+    ids = list(range(B))
+    for i in ids:
+        pool.blocks.allocate(i, np.arange(int(L[i]) - 1), cache_salt=f"seq{i}")
+    slots = pool.append_slots(ids)
+    bt, lens = pool.blocks.tables(ids)
+    n_used = int(bt.max()) + 1
+    qs, ks, vs, outs = [], [], [], []
+    for c in pool.layers:
+        if kv_dtype == "bf16":
+            c.k[:n_used].normal_(generator=gen)
+            c.v[:n_used].normal_(generator=gen)
+        else:
+            for t in (c.k, c.v):
+                t[:n_used].copy_(torch.randint(0, 256, t[:n_used].shape, generator=gen, device=dev,
+                                               dtype=torch.int32).to(torch.uint8) & 0xF7)
+            c.k_scale.fill_(2.0 ** -8)
+            c.v_scale.fill_(2.0 ** -8)
+        qs.append(torch.randn((B, HQ, D), generator=gen, device=dev).to(torch.bfloat16))
+        ks.append(torch.randn((B, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
+        vs.append(torch.randn((B, HKV, D), generator=gen, device=dev).to(torch.bfloat16))
+        outs.append(torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev))
+    step = DecodeStep(pool.layers, qs, ks, vs, outs, torch.from_numpy(bt).to(dev), torch.from_numpy(lens).to(dev),
+                      slots, w.scale, max_seq_len=int(lens.max()), partition_size=args.partition)
+    shared = pool.decode_shares_blocks(ids)
+    w2 = dataclasses.replace(w, num_blocks=pool.num_blocks, block_tables=bt,
+                             context_lens=lens.astype(w.context_lens.dtype))
+    return _StepWithPolicy(step, shared), pool.nbytes // args.layers, w2, pool
 
 
 def gqa_plan(torch, dev, w, caches, qs, ks, vs, outs, partition: int = 0, grouped: bool = False):
@@ -281,13 +367,22 @@ def workload(args, torch, dev) -> dict:
 
     name = args.workload
     kv_dtype = getattr(args, "kv_dtype", None)
+    stream = None  # the decode's read policy, when the step chooses it
     if name in ("qwen3-4b", "qwen3-4b-var"):
         w = synth.qwen3_4b_workload(batch=args.batch, context=args.context if name == "qwen3-4b" else None)
         args.layers = args.layers or 36
         kv_dtype = kv_dtype or "bf16"
-        step, cache_bytes = _gqa_setup(torch, dev, args, w, kv_dtype)
-        kv_bytes = 1 if kv_dtype == "fp8_e4m3" else 2
         desc = f"Qwen3-4B decode step: 36 layers x (append 1 token/seq + GQA paged decode attention), {kv_dtype} KV"
+        if getattr(args, "via_pool", False):
+            step, cache_bytes, w, _pool = _gqa_pool_setup(torch, dev, args, w, kv_dtype)
+            stream = not step.shared_blocks
+            desc += (", through KVPool.from_engine_config(gpu_memory_utilization=0.35) with block-manager tables "
+                     f"and the per-step read policy ({'streamed' if stream else 'cached'})")
+        else:
+            step, cache_bytes = _gqa_setup(torch, dev, args, w, kv_dtype)
+        kv_bytes = 1 if kv_dtype == "fp8_e4m3" else 2
+    elif getattr(args, "via_pool", False):
+        raise SystemExit("--via-pool applies to the qwen3-4b and qwen3-4b-var workloads")
     elif name == "qwen2.5-0.5b":
         w = synth.qwen25_05b_workload()
         args.layers = args.layers or 24
@@ -436,7 +531,8 @@ def workload(args, torch, dev) -> dict:
                        if getattr(step, "grouped", False) else f"decode_gqa_kernel<{D},{f8},true,W>"),
             "dtype": "fp8_e4m3 KV, bf16 q/o" if kv_bytes == 1 else "bf16", "desc": desc, "kv_dtype": kv_dtype,
             "flops_per_layer": 4 * int(L.sum()) * HQ * D, "cache_bytes": cache_bytes,
-            "logical_kv_bytes": int(L.sum()) * 2 * HKV * D * kv_bytes}
+            "logical_kv_bytes": int(L.sum()) * 2 * HKV * D * kv_bytes,
+            "stream": (w.group_size == 1) if stream is None else stream}
 
 
 def phase_clocks(args) -> int:
@@ -520,20 +616,38 @@ def main() -> int:
     print(f"# setup done: {wl['name']}, {args.layers} layers x {wl['cache_bytes'] / 2**30:.2f} GiB cache",
           file=sys.stderr, flush=True)
 
-    for _ in range(args.warmup):
-        step.run()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_wall = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        step.run()
-    e1.record()
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter() - t_wall
-    ms_per_step = e0.elapsed_time(e1) / args.steps
-    print(f"# timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {t_wall / args.steps * 1e3:.2f} ms/step)",
+    def timed(run) -> tuple[float, float]:
+        for _ in range(args.warmup):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps, (time.perf_counter() - t0) / args.steps * 1e3
+
+    ms_per_step, wall_ms = timed(step.run)
+    print(f"# timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step (wall {wall_ms:.2f} ms/step)",
           file=sys.stderr, flush=True)
+    graph_rec = None
+    if args.graph:
+        from wavelet_amd.plan import DecodeStep, GraphDecodeStep
+
+        plain = step.step if hasattr(step, "shared_blocks") else step
+        if not isinstance(plain, DecodeStep) or plain.grouped:
+            print("--graph applies to the plain GQA decode workloads", file=sys.stderr)
+            return 2
+        graph = GraphDecodeStep(plain, shared_blocks=getattr(step, "shared_blocks", None))
+        eager_ms = ms_per_step
+        ms_per_step, wall_ms = timed(graph.replay)
+        graph_rec = {"us_per_step_replayed": round(ms_per_step * 1e3, 1), "us_per_step_eager": round(eager_ms * 1e3, 1),
+                     "launch": "one HIP graph per step: decode order + every layer's allocation-free fused "
+                               "append + attention (wkv_append_paged_decode_gqa_noalloc)"}
+        print(f"# graph replays: {ms_per_step * 1e3:.1f} us/step (eager {eager_ms * 1e3:.1f})", file=sys.stderr,
+              flush=True)
 
     # Per-launch timing of one layer's step (fused append + attention for GQA),
     # layer caches rotated so no layer is re-read from cache.
@@ -589,7 +703,7 @@ def main() -> int:
         from wavelet_amd import decode_plan
 
         _, waves, _ = decode_plan(w.batch, w.num_kv_heads, int(w.context_lens.max()), w.block_size, args.partition)
-        stream = "false" if w.group_size > 1 else "true"  # shared prompt blocks keep the default read policy
+        stream = "true" if wl["stream"] else "false"  # shared prompt blocks keep the default read policy
         kernel_name = kernel_name.replace(",W>", f",{waves},{stream}>")
     rec = {
         "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx" if headline
@@ -631,8 +745,12 @@ def main() -> int:
         "hbm_read_ceiling": {"kernel": "hbm_read_probe_kernel (16-byte loads, 8 in flight per lane)",
                              "bytes": ceiling["bytes"], "workgroups": ceiling["workgroups"]},
     }
+    if args.via_pool:
+        rec["config"]["via_pool"] = True
+    if graph_rec is not None:
+        rec["graph"] = graph_rec
     traffic, source = measured_traffic(wl["name"], wl.get("kv_dtype", ""), kernel_name)
-    if traffic is not None and args.layers == ({"qwen3-4b": 36, "qwen3-4b-var": 36, "qwen2.5-0.5b": 24,
+    if traffic is not None and not args.via_pool and args.layers == ({"qwen3-4b": 36, "qwen3-4b-var": 36, "qwen2.5-0.5b": 24,
                                                 "deepseek-v3-mla": 8}
                                                .get(wl["name"], -1)) and args.partition == 0:
         rec["roofline"]["traffic"] = traffic
@@ -641,7 +759,7 @@ def main() -> int:
         rec["unfused_us"] = {"append": round(append_us, 2), "attention": round(attend_us, 2)}
     if "logical_kv_bytes" in wl and wl["w"].group_size > 1:
         rec["config"]["logical_kv_bytes_per_layer"] = wl["logical_kv_bytes"]
-    if headline and not args.no_cpu_baseline:
+    if headline and not args.no_cpu_baseline and not args.via_pool:
         rec["cpu_baseline"] = cpu_baseline(args, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size, w.scale,
                                            wl["layer_bytes"])
     print(json.dumps(rec), flush=True)

@@ -134,10 +134,34 @@ int wkv_gather(const wkv_cache_t *cache, const int32_t *block_table, int64_t bt_
                int32_t batch, void *out_k, void *out_v, int32_t dequant, void *stream);
 
 /* Copy whole blocks (K, V and fp8 scales): for i < n, block mapping[2i+1]
- * becomes a copy of block mapping[2i]. Copy-on-write of a partially filled
- * shared block when a GRPO group forks (n = num_generations sampling,
- * engine.py:69-90). Replaces vLLM copy_blocks. */
+ * becomes a copy of block mapping[2i]. The pairs are copied concurrently, so
+ * they must be independent: no block may be the destination of one pair and
+ * the source or destination of another (the block manager's copy-on-write
+ * pairs -- a shared block, a fresh one -- never are). Copy-on-write of a
+ * partially filled shared block when a GRPO group forks (n = num_generations
+ * sampling, engine.py:69-90). Replaces vLLM copy_blocks. */
 int wkv_copy_blocks(const wkv_cache_t *cache, const int64_t *block_mapping, int64_t n, void *stream);
+
+/* MLA latent gather: contiguous copy of each sequence's latent rows,
+ *   out[cu_seq_lens[i] + t] = latent[block_table[i, t / bs], t % bs], t < seq_lens[i]
+ * out: [sum(seq_lens), kv_lora_rank + rope_dim] bf16, rows as stored (c_kv
+ * then k_pe). Table arguments as for wkv_gather; an entry outside
+ * [0, num_blocks) leaves its rows unwritten. Replaces vLLM gather_cache on the
+ * MLA latent cache (the cached-context read of MLA chunked prefill and of
+ * prefix-cache hits inside llm.generate, engine.py:887); index semantics of
+ * the latent gather at wavelet/trainer/models/deepseek_v4/attention.py:85-88
+ * and :320-360. */
+int wkv_mla_gather(const wkv_mla_cache_t *cache, const int32_t *block_table, int64_t bt_stride,
+                   int32_t max_blocks_per_seq, const int32_t *seq_lens, const int64_t *cu_seq_lens, int32_t batch,
+                   void *out, void *stream);
+
+/* Copy whole latent blocks: for i < n, block mapping[2i+1] becomes a copy of
+ * block mapping[2i] (pairs naming a block outside [0, num_blocks) are
+ * skipped; pairs independent, as for wkv_copy_blocks). Copy-on-write of a
+ * shared, partly filled latent block before a
+ * GRPO group member appends into it (n = num_generations sampling,
+ * engine.py:69-90). Replaces vLLM copy_blocks on an MLA cache. */
+int wkv_mla_copy_blocks(const wkv_mla_cache_t *cache, const int64_t *block_mapping, int64_t n, void *stream);
 
 /* ---- paged decode attention ---------------------------------------------
  * o[b, h] = softmax(q[b, h] . K_b^T * scale) . V_b over seq_lens[b] tokens read
@@ -373,6 +397,31 @@ int wkv_append_paged_decode_mla(const wkv_mla_cache_t *cache, const void *kv_c, 
                                 const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
                                 const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
                                 int32_t partition_size, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* The two MLA decode calls with a per-head attention sink: sinks[h] (fp32,
+ * device memory, one per query head, natural-log units like the scaled
+ * scores; -inf = none) is one more logit in head h's softmax whose value
+ * vector is zero, so o[b, h] = sum_t e^(s_t) c_t / (sum_t e^(s_t) + e^(sinks[h]))
+ * and a zero-length sequence still gives zeros. Otherwise the arguments and
+ * behaviour of wkv_paged_decode_mla / wkv_append_paged_decode_mla. Replaces
+ * the learned per-head sink of the reference's shared-KV MQA attention
+ * (wavelet/trainer/models/deepseek_v4/attention.py:703 declares it, :89-95
+ * and :763 add it to the softmax), which its MLA decode backend must honour. */
+int wkv_paged_decode_mla_sinks(const wkv_mla_cache_t *cache, const void *q_nope, int64_t qn_stride_b,
+                               int64_t qn_stride_h, const void *q_pe, int64_t qp_stride_b, int64_t qp_stride_h,
+                               void *out, int32_t num_heads, const int32_t *block_table, int64_t bt_stride,
+                               int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                               int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
+                               int64_t workspace_bytes, const float *sinks, void *stream);
+
+int wkv_append_paged_decode_mla_sinks(const wkv_mla_cache_t *cache, const void *kv_c, int64_t kv_c_stride,
+                                      const void *k_pe, int64_t k_pe_stride, const int64_t *slot_mapping,
+                                      const void *q_nope, int64_t qn_stride_b, int64_t qn_stride_h,
+                                      const void *q_pe, int64_t qp_stride_b, int64_t qp_stride_h, void *out,
+                                      int32_t num_heads, const int32_t *block_table, int64_t bt_stride,
+                                      int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                                      int32_t max_seq_len, float scale, int32_t partition_size, void *workspace,
+                                      int64_t workspace_bytes, const float *sinks, void *stream);
 
 /* ---- measurement --------------------------------------------------------
  * Read `bytes` (a multiple of 16) of device memory at `buf` once, with

@@ -184,6 +184,55 @@ def gather(k_phys, v_phys, block_table, seq_lens):
     return np.concatenate(outs_k), np.concatenate(outs_v)
 
 
+def copy_blocks(arrays, pairs) -> None:
+    """Copy-on-write block copies, in place: for each ``(src, dst)``, block
+    ``dst`` of every array (K, V, scales, or an MLA latent cache; block index
+    on axis 0) becomes a copy of block ``src``; pairs naming a block outside
+    ``[0, num_blocks)`` are skipped. Pairs are independent -- no block is the
+    destination of one pair and the source or destination of another, as the
+    block manager's pairs (a shared block, a fresh one) never are -- so every
+    copy reads the blocks as they were before the call. vLLM's
+    ``copy_blocks``, applied before a GRPO member writes into a prompt block it
+    still shares (``SamplingParams(n=...)``, wavelet/inference/engine.py:69-90)."""
+    m = np.asarray(pairs, dtype=np.int64).reshape(-1, 2)
+    dsts = [int(d) for _, d in m]
+    if len(set(dsts)) != len(dsts) or set(dsts) & {int(s) for s, _ in m}:
+        raise ValueError("copy pairs must be independent (a destination is never another pair's block)")
+    for a in arrays:
+        before = a.copy()
+        for src, dst in m:
+            if 0 <= src < a.shape[0] and 0 <= dst < a.shape[0]:
+                a[dst] = before[src]
+
+
+def append_mla(latent, kv_c_bits, k_pe_bits, slot_mapping) -> None:
+    """``latent.view(NB*BS, R+P)[slot[t]] = concat(kv_c[t], k_pe[t])`` for every
+    ``slot[t] >= 0`` (in place): vLLM's ``concat_and_cache_mla`` on the
+    ``[NB, BS, R + P]`` latent layout (the row the DSV4 shared-KV attention
+    keeps per token, wavelet/trainer/models/deepseek_v4/attention.py:652-663)."""
+    nb, bs, w = latent.shape
+    r = kv_c_bits.shape[1]
+    flat = latent.reshape(nb * bs, w)
+    for t, slot in enumerate(np.asarray(slot_mapping, dtype=np.int64)):
+        if 0 <= slot < nb * bs:
+            flat[slot, :r] = kv_c_bits[t]
+            flat[slot, r:] = k_pe_bits[t]
+
+
+def gather_mla(latent, block_table, seq_lens) -> np.ndarray:
+    """Contiguous ``[sum L, R + P]`` copy of each sequence's latent rows:
+    ``out[i, t] = latent[bt[i, t // BS], t % BS]`` for ``t < seq_lens[i]`` (the
+    index read of ``SparseAttnInputs``, attention.py:320-360, and the gather of
+    attention.py:85-88 over the shared latent); entries past ``seq_lens[i]`` are
+    never read. Raw stored elements (bf16 bits)."""
+    bs, w = latent.shape[1], latent.shape[2]
+    parts = []
+    for i, length in enumerate(np.asarray(seq_lens, dtype=np.int64)):
+        pos = np.arange(length)
+        parts.append(latent[np.asarray(block_table[i], dtype=np.int64)[pos // bs], pos % bs])
+    return np.concatenate(parts) if parts else np.zeros((0, w), latent.dtype)
+
+
 def dequant_gathered(codes: np.ndarray, scales: np.ndarray, block_table, seq_lens, block_size) -> np.ndarray:
     """fp8 codes from ``gather`` -> fp32 values, scale of each token's (block, head)."""
     parts = []
@@ -291,14 +340,18 @@ def prefill_gqa(q, k_vals, v_vals, block_table, seq_lens, cu_seqlens_q, scale, *
     return out
 
 
-def decode_mla(q, latent_vals, block_table, seq_lens, scale, kv_lora_rank=512, *, p_bf16=False, dtype=np.float64):
+def decode_mla(q, latent_vals, block_table, seq_lens, scale, kv_lora_rank=512, *, p_bf16=False, dtype=np.float64,
+               sinks=None):
     """Weight-absorbed MLA decode over a single latent head.
 
     ``q`` ``[B, H, R + P]`` (absorbed ``q_nope @ W_UK`` then ``q_pe``),
     ``latent_vals`` logical ``[NB, BS, R + P]`` (``c_kv`` then ``k_pe``):
     ``s = q . c^T * scale``; ``o_lat = softmax(s) . c[:, :R]``. Every query
     head shares the one latent entry, as the DSV4 shared-KV MQA does
-    (attention.py:652-663, 744-771). Returns ``[B, H, R]``.
+    (attention.py:652-663, 744-771). ``sinks`` (``[H]``, natural-log logits,
+    ``-inf`` = none) adds each head's zero-value sink logit to its softmax, as
+    that attention's per-head ``sinks`` (attention.py:703, used at :89-95 and
+    :763) do. A zero-length sequence gives zeros. Returns ``[B, H, R]``.
     """
     q = np.asarray(q)
     b, h, w = q.shape
@@ -311,7 +364,8 @@ def decode_mla(q, latent_vals, block_table, seq_lens, scale, kv_lora_rank=512, *
         pos = np.arange(length)
         blk = np.asarray(block_table[i], dtype=np.int64)[pos // bs]
         c = latent_vals[blk, pos % bs].astype(dtype)  # [L, R+P]
-        p = _softmax_rows((q[i].astype(dtype) @ c.T) * dtype(scale))
+        p = _softmax_rows((q[i].astype(dtype) @ c.T) * dtype(scale),
+                          None if sinks is None else np.asarray(sinks, dtype=dtype))
         if p_bf16:
             p = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(dtype)
         out[i] = p @ c[:, :kv_lora_rank]

@@ -267,3 +267,54 @@ def test_sample_gather_copy_reject_bad_arguments_before_launch():
     assert lib.wkv_copy_blocks(ctypes.byref(d), None, -1, None) == _lib.WKV_ERR_INVALID
     assert lib.wkv_copy_blocks(ctypes.byref(d), None, 1, None) == _lib.WKV_ERR_INVALID
     assert lib.wkv_copy_blocks(ctypes.byref(d), None, 0, None) == _lib.WKV_OK
+
+
+@host_only
+def test_cache_descriptor_flags_and_reserved_are_checked():
+    """Unknown flag bits and a non-zero `reserved` are refused (wkv.h documents both),
+    so a caller built against an older or newer descriptor cannot pass garbage."""
+    lib = _lib.load()
+    for kw in (dict(flags=2), dict(flags=-1), dict(reserved=1)):
+        d = _desc(**kw)
+        assert lib.wkv_copy_blocks(ctypes.byref(d), 16, 1, None) == _lib.WKV_ERR_INVALID
+        assert "flags" in _lib.last_error() or "reserved" in _lib.last_error()
+    d = _desc(flags=_lib.CACHE_SHARED_BLOCKS)
+    assert lib.wkv_copy_blocks(ctypes.byref(d), 16, 0, None) == _lib.WKV_OK
+
+
+@host_only
+def test_mla_gather_copy_and_sinks_reject_bad_arguments_before_launch():
+    lib = _lib.load()
+    m = _lib.WkvMlaCache(latent=16, num_blocks=4, block_size=64, kv_lora_rank=512, rope_dim=64)
+    g = lib.wkv_mla_gather
+
+    def gather(bt=16, bts=4, mb=4, sl=16, cu=16, batch=2, out=16, cache=m):
+        return g(ctypes.byref(cache), bt, bts, mb, sl, cu, batch, out, None)
+
+    assert gather(batch=-1) == _lib.WKV_ERR_INVALID
+    assert gather(bts=2) == _lib.WKV_ERR_INVALID
+    assert gather(bt=None) == _lib.WKV_ERR_INVALID
+    assert gather(cu=None) == _lib.WKV_ERR_INVALID
+    assert gather(out=None) == _lib.WKV_ERR_INVALID
+    assert gather(out=24) == _lib.WKV_ERR_INVALID  # not 16-byte aligned
+    assert gather(batch=0) == _lib.WKV_OK
+    bad = _lib.WkvMlaCache(latent=16, num_blocks=4, block_size=40, kv_lora_rank=512, rope_dim=64)
+    assert gather(cache=bad) == _lib.WKV_ERR_INVALID
+    assert lib.wkv_mla_gather(None, 16, 4, 4, 16, 16, 2, 16, None) == _lib.WKV_ERR_INVALID
+    c = lib.wkv_mla_copy_blocks
+    assert c(ctypes.byref(m), None, -1, None) == _lib.WKV_ERR_INVALID
+    assert c(ctypes.byref(m), None, 1, None) == _lib.WKV_ERR_INVALID
+    assert c(ctypes.byref(m), None, 0, None) == _lib.WKV_OK
+    assert c(ctypes.byref(bad), 16, 1, None) == _lib.WKV_ERR_INVALID
+    # sinks: NULL or misaligned sinks refused; otherwise the plain call's checks
+    d = lib.wkv_paged_decode_mla_sinks
+    args = (16, 0, 0, 16, 0, 0, 16, 128, 16, 1, 1, 16, 1, 64, 0.1, 0, None, 0)
+    assert d(ctypes.byref(m), *args, None, None) == _lib.WKV_ERR_INVALID
+    assert d(ctypes.byref(m), *args, 18, None) == _lib.WKV_ERR_INVALID
+    m256 = _lib.WkvMlaCache(latent=16, num_blocks=4, block_size=64, kv_lora_rank=256, rope_dim=64)
+    assert d(ctypes.byref(m256), *args, 16, None) == _lib.WKV_ERR_UNSUPPORTED
+    f = lib.wkv_append_paged_decode_mla_sinks
+    fargs = (16, 512, 16, 64, 16, 16, 0, 0, 16, 0, 0, 16, 128, 16, 1, 1, 16, 1, 64, 0.1, 0, None, 0)
+    assert f(ctypes.byref(m), *fargs, None, None) == _lib.WKV_ERR_INVALID
+    assert f(ctypes.byref(m), None, *fargs[1:], 16, None) == _lib.WKV_ERR_INVALID
+    assert f(ctypes.byref(m), 16, 512, 16, 64, None, *fargs[5:], 16, None) == _lib.WKV_ERR_INVALID

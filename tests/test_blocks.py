@@ -131,3 +131,79 @@ def test_validate_group_prefix_accepts_true_claims_and_names_false_ones():
     validate_group_prefix(bt, short, np.array([1000, 64, 64], np.int32), 4, 16)  # cut to the shortest member
     with pytest.raises(ValueError, match="one entry per group"):
         validate_group_prefix(bt, lens, ok[:2], 4, 16)
+
+
+def _state(m, ids):
+    return ([m.blocks_of(s) for s in ids], [m.seq_len(s) for s in ids], m.num_free_blocks,
+            [m.ref_count(b) for b in range(m.num_blocks)])
+
+
+def test_multi_token_append_slots_follow_each_table_and_copy_once():
+    m = BlockManager(64, 16)
+    m.allocate("p", np.arange(40))  # the third block is partly filled
+    m.fork("p", "c")
+    last = m.blocks_of("p")[2]
+    slots, cow = m.append_slots(["c", "p"], 20)  # 8 + 12 tokens: fills the third block, opens a fourth
+    assert cow == [(last, m.blocks_of("c")[2])]
+    for i, sid in enumerate(["c", "p"]):
+        table = np.asarray(m.blocks_of(sid), np.int64)
+        pos = np.arange(40, 60)
+        np.testing.assert_array_equal(slots[i * 20:(i + 1) * 20], table[pos // 16] * 16 + pos % 16)
+        assert m.seq_len(sid) == 60 and len(table) == 4
+    assert m.ref_count(last) == 1 and m.blocks_of("p")[2] == last
+    assert m.blocks_needed(["c", "p"], 0) == 0
+
+
+def test_append_slots_changes_nothing_when_the_step_cannot_be_taken():
+    m = BlockManager(8, 16, max_model_len=64)
+    m.allocate("a", np.arange(30))
+    m.fork("a", "b")
+    m.allocate("c", np.arange(60))
+    before = _state(m, ["a", "b", "c"])
+    with pytest.raises(ValueError, match="max_model_len"):
+        m.append_slots(["a", "b", "c"], 5)  # c would reach 65
+    assert _state(m, ["a", "b", "c"]) == before
+    # a and b need a copy of their shared partial block plus fresh ones: more than the free pool
+    assert m.blocks_needed(["a", "b"], 30) > m.num_free_blocks
+    with pytest.raises(MemoryError):
+        m.append_slots(["a", "b"], 30)
+    assert _state(m, ["a", "b", "c"]) == before
+    with pytest.raises(ValueError, match="twice"):
+        m.append_slots(["a", "a"])
+    assert _state(m, ["a", "b", "c"]) == before
+    # the same step within the limits goes through
+    slots, cow = m.append_slots(["a", "b"], 2)
+    assert len(slots) == 4 and len(cow) == 1
+
+
+def test_blocks_needed_counts_exactly_what_append_slots_takes():
+    rng = np.random.default_rng(5)
+    for trial in range(30):
+        m = BlockManager(400, 16)
+        ids = []
+        for g in range(4):
+            n = int(rng.integers(1, 60))
+            m.allocate(f"g{g}", np.arange(n) + 1000 * trial + 100 * g)
+            ids.append(f"g{g}")
+            for j in range(int(rng.integers(0, 4))):
+                m.fork(f"g{g}", f"g{g}.{j}")
+                ids.append(f"g{g}.{j}")
+        rng.shuffle(ids)
+        n = int(rng.integers(1, 40))
+        need = m.blocks_needed(ids, n)
+        free = m.num_free_blocks
+        m.append_slots(ids, n)
+        assert free - m.num_free_blocks == need
+
+
+def test_any_shared_follows_reference_counts():
+    m = BlockManager(64, 16)
+    m.allocate("a", np.arange(20))
+    m.allocate("x", np.arange(40) + 99)
+    assert not m.any_shared(["a", "x"])
+    m.fork("a", "b")
+    assert m.any_shared(["a"]) and m.any_shared(["b", "x"])
+    m.append_slots(["a", "b"], 20)  # b copies the partial block; the full first block stays shared
+    assert m.any_shared(["a", "b"])
+    m.free("b")
+    assert not m.any_shared(["a", "x"])

@@ -1,12 +1,14 @@
 """Parity at the launch plans the benchmark times, at the workloads' full sizes.
 
-Every plan here is built by the benchmark's own constructor call
-(``bench.gqa_plan`` / ``bench.mla_plan``: fused append + attention, the
+Every plan here is built by the benchmark's own constructor calls
+(``bench.gqa_cache`` -- the caches and their read policy -- then
+``bench.gqa_plan`` / ``bench.mla_plan``: fused append + attention, the
 library's partition, dispatch order and waves per workgroup) on two layers of
 the full-size workload, so the kernel instantiations and launch shapes under
 test are the ones the bench line reports -- e.g. the headline's
-``decode_gqa_kernel<128,false,true,8>`` with 512-token partitions and one
-workgroup per (sequence, KV head), no merge.
+``decode_gqa_kernel<128,false,true,8,true>`` (streamed reads) with 512-token
+partitions and one workgroup per (sequence, KV head), no merge, and the fp8
+groups' kernels with the cached read policy of shared prompt blocks.
 
 Per layer, after one ``run()``:
 
@@ -39,7 +41,7 @@ import torch
 import bench
 from kvcase import Guarded, assert_guards, bits_of, check_attention, guard_cache, guarded_workspace
 from oracle import fp8, paged
-from wavelet_amd import MLALatentCache, PagedKVCache, _lib, decode_plan, synth
+from wavelet_amd import MLALatentCache, _lib, decode_plan, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -94,7 +96,8 @@ def _gqa_buffers(cuda, w, kv_dtype: str, std: float):
     own = torch.from_numpy(_owned(w)).to(cuda)
     caches, guards, qs, ks, vs, outs = [], [], [], [], [], []
     for _ in range(LAYERS):
-        c = PagedKVCache(w.num_blocks, BS, HKV, D, kv_dtype=kv_dtype, device=cuda)
+        c = bench.gqa_cache(w, kv_dtype, cuda)  # the bench's own caches (and read policy)
+        assert c.shared_blocks == (w.group_size > 1)
         if kv_dtype == "bf16":
             c.k.normal_(generator=gen).mul_(std)
             c.v.normal_(generator=gen).mul_(std)

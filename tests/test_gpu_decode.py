@@ -258,12 +258,14 @@ def test_fused_mla_append_decode_equals_append_then_decode(cuda, heads, bs, part
     print(f"fused mla heads={heads} bs={bs} P={partition}: err abs {a:.2e} rel {r:.2e}")
 
 
+@pytest.mark.parametrize("shared", [False, True])
 @pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("hq,hkv,d,bs", [(32, 8, 128, 16), (14, 2, 64, 16), (16, 4, 128, 64)])
-def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, d, bs):
+def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, d, bs, shared):
     """One launch (append + attention) leaves the cache bit-identical to wkv_append(_fp8) and
     attends within tolerance (bf16 attends the new token from its inputs, a different summation
-    order; fp8 reads it back from the cache, so there the outputs are bit-identical too)."""
+    order; fp8 reads it back from the cache, so there the outputs are bit-identical too). Both
+    read policies (``shared``: K/V kept cached, else streamed), one-workgroup and merged plans."""
     lens = np.array([1, 2, 16, 17, 64, 65, 300, 1024, 1025, 2000])
     w = synth.make_decode_workload(f"fused{kv_dtype}{hq}{bs}", batch=len(lens), num_kv_heads=hkv, num_q_heads=hq,
                                    head_dim=d, block_size=bs, context_lens=lens)
@@ -284,9 +286,9 @@ def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, 
     sl = torch.from_numpy(w.context_lens).to(cuda)
     for p in (0, 4 * bs):
         caches[0].append(kn, vn, nslots)
-        ref_out = paged_decode_gqa(q, caches[0], bt, sl, w.scale, partition_size=p)
+        ref_out = paged_decode_gqa(q, caches[0], bt, sl, w.scale, partition_size=p, shared_blocks=shared)
         out = paged_decode_gqa(q, caches[1], bt, sl, w.scale, partition_size=p, new_key=kn, new_value=vn,
-                               slot_mapping=nslots)
+                               slot_mapping=nslots, shared_blocks=shared)
         torch.cuda.synchronize()
         assert torch.equal(caches[0].k.view(torch.uint8), caches[1].k.view(torch.uint8)), f"K differs (P={p})"
         assert torch.equal(caches[0].v.view(torch.uint8), caches[1].v.view(torch.uint8)), f"V differs (P={p})"
@@ -326,11 +328,12 @@ def test_decode_matches_golden_output(cuda, golden_dir):
     check_attention(got, np.load(golden_dir / "gqa_decode.npz")["out"], "golden gqa")
 
 
+@pytest.mark.parametrize("shared", [False, True])
 @pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
-def test_grpo_group_decode_with_block_manager(cuda, kv_dtype):
+def test_grpo_group_decode_with_block_manager(cuda, kv_dtype, shared):
     """A GRPO group end to end: one prompt (partial last block) shared by 8 members through the
     block manager, copy-on-write of the shared partial block, three fused decode steps; caches
-    bit-exact against the oracle's, attention within tolerance."""
+    bit-exact against the oracle's, attention within tolerance, under both read policies."""
     from wavelet_amd import BlockManager
 
     H, HQ, D, BS, NB = 4, 28, 128, 16, 256
@@ -375,7 +378,8 @@ def test_grpo_group_decode_with_block_manager(cuda, kv_dtype):
             paged.append_bf16(kc, vc, kn, vn, slots)
         out = paged_decode_gqa(to_dev_bits(q, BF16, cuda), cache, torch.from_numpy(bt).to(cuda),
                                torch.from_numpy(lens).to(cuda), scale, new_key=to_dev_bits(kn, BF16, cuda),
-                               new_value=to_dev_bits(vn, BF16, cuda), slot_mapping=torch.from_numpy(slots).to(cuda))
+                               new_value=to_dev_bits(vn, BF16, cuda), slot_mapping=torch.from_numpy(slots).to(cuda),
+                               shared_blocks=shared)
         assert np.array_equal(bits_of(cache.k), kc) and np.array_equal(bits_of(cache.v), vc), f"cache step {step}"
         if is_fp8:
             np.testing.assert_array_equal(cache.k_scale.cpu().numpy(), ks)

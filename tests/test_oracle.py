@@ -537,3 +537,165 @@ def test_prefill_gqa_sinks_consistent_with_decode():
     none = paged.prefill_gqa(q, kv, vv, w.block_tables, w.context_lens, cu, w.scale)
     np.testing.assert_array_equal(
         paged.prefill_gqa(q, kv, vv, w.block_tables, w.context_lens, cu, w.scale, sinks=np.full(8, -np.inf)), none)
+
+
+# ---------------------------------------------------------------------------
+# MLA latent cache: append / gather / block copy, and sinks in the MLA decode
+
+def _mla_tables(lens, bs, num_blocks, seed):
+    """Block tables dealing a seeded permutation of the pool's blocks to the sequences."""
+    perm = np.random.default_rng(seed).permutation(num_blocks).astype(np.int32)
+    width = max(-(-int(L) // bs) for L in lens)
+    bt = np.full((len(lens), width), -1, np.int32)
+    k = 0
+    for i, L in enumerate(lens):
+        n = -(-int(L) // bs)
+        bt[i, :n] = perm[k:k + n]
+        k += n
+    return bt
+
+
+def test_mla_append_gather_round_trip_and_untouched_blocks():
+    nb, bs, r, p = 40, 16, 32, 8
+    lens = np.array([1, 16, 17, 100, 63, 0, 200], np.int32)
+    bt = _mla_tables(lens, bs, nb, 3)
+    lat = np.full((nb, bs, r + p), 0xFFC1, np.uint16)  # a NaN pattern in every unwritten element
+    before = lat.copy()
+    slots = np.concatenate([bt[i][np.arange(L) // bs].astype(np.int64) * bs + np.arange(L) % bs
+                            for i, L in enumerate(lens)])
+    kvc = synth.normal_bf16(synth.stream_key("mlart", "c"), (len(slots), r))
+    kpe = synth.normal_bf16(synth.stream_key("mlart", "p"), (len(slots), p))
+    paged.append_mla(lat, kvc, kpe, slots)
+    got = paged.gather_mla(lat, bt, lens)
+    np.testing.assert_array_equal(got, np.concatenate([kvc, kpe], axis=1))
+    used = set((slots // bs).tolist())
+    free = [b for b in range(nb) if b not in used]
+    np.testing.assert_array_equal(lat[free], before[free])
+    assert paged.gather_mla(lat, bt[:0], lens[:0]).shape == (0, r + p)
+
+
+def test_mla_append_and_gather_match_elementwise_loops():
+    nb, bs, r, p = 5, 16, 16, 8
+    lat = np.zeros((nb, bs, r + p), np.uint16)
+    slots = np.array([17, -1, 3, 79, 40, 16], np.int64)
+    kvc = synth.normal_bf16(synth.stream_key("mlaloop", "c"), (len(slots), r))
+    kpe = synth.normal_bf16(synth.stream_key("mlaloop", "p"), (len(slots), p))
+    paged.append_mla(lat, kvc, kpe, slots)
+    expect = np.zeros_like(lat)
+    for t, s in enumerate(slots):
+        if s < 0:
+            continue
+        b, o = divmod(int(s), bs)
+        for e in range(r + p):
+            expect[b, o, e] = kvc[t, e] if e < r else kpe[t, e - r]
+    np.testing.assert_array_equal(lat, expect)
+    bt = np.array([[1, 4, 0], [2, 0, 0]], np.int32)
+    lens = np.array([35, 7], np.int32)
+    got = paged.gather_mla(lat, bt, lens)
+    row = 0
+    for i in range(2):
+        for t in range(int(lens[i])):
+            for e in range(r + p):
+                assert got[row, e] == lat[bt[i, t // bs], t % bs, e]
+            row += 1
+    assert row == got.shape[0]
+
+
+def test_copy_blocks_is_copy_on_write():
+    """After (src, dst) copies, a table that names dst where it named src gathers the
+    same context (what a forked member's own table then reads), one source may feed
+    several destinations, out-of-range pairs change nothing, and chained pairs are refused."""
+    nb, bs, r, p = 12, 16, 16, 8
+    lat = synth.random_u64(synth.stream_key("cow", "lat"), nb * bs * (r + p)).astype(np.uint16).reshape(nb, bs, r + p)
+    ks = np.arange(nb * 2, dtype=np.float32).reshape(nb, 2)
+    orig, orig_ks = lat.copy(), ks.copy()
+    paged.copy_blocks([lat, ks], [(3, 9), (3, 10), (-1, 2), (4, nb)])
+    for b in range(nb):
+        src = 3 if b in (9, 10) else b
+        np.testing.assert_array_equal(lat[b], orig[src])
+        np.testing.assert_array_equal(ks[b], orig_ks[src])
+    with pytest.raises(ValueError, match="independent"):
+        paged.copy_blocks([lat], [(3, 9), (9, 10)])
+    with pytest.raises(ValueError, match="independent"):
+        paged.copy_blocks([lat], [(3, 9), (4, 9)])
+    bt = np.array([[5, 3, 7]], np.int32)
+    lens = np.array([40], np.int32)
+    np.testing.assert_array_equal(paged.gather_mla(lat, np.array([[5, 9, 7]], np.int32), lens),
+                                  paged.gather_mla(lat, bt, lens))
+
+
+def mla_sink_case():
+    """The reference's known answer as a shared-KV (MLA) decode with its sink.
+
+    tests/test_deepseek_attention.py:100-118: query [0.5, -0.25], one key that is
+    also the value [2, -1] (the shared-KV attention of attention.py:652-663 reads
+    one latent row as key and value), scaling 0.5, a zero-logit zero-value sink,
+    an ignored slot: output sigmoid(0.625) * [2, -1]. Here the latent row is
+    c_kv = [2, -1, 0...], k_pe = 0; every slot past the one-token context holds NaN.
+    """
+    nb, bs, r, p = 2, 16, 16, 8
+    lat = np.full((nb, bs, r + p), np.nan)
+    lat[1, 0] = 0.0
+    lat[1, 0, :2] = [2.0, -1.0]
+    q = np.zeros((1, 1, r + p))
+    q[0, 0, :2] = [0.5, -0.25]
+    expected = np.zeros((1, 1, r))
+    expected[0, 0, :2] = (1.0 / (1.0 + math.exp(-0.625))) * np.array([2.0, -1.0])
+    return lat, q, np.array([[1]], np.int32), np.array([1], np.int32), 0.5, np.zeros(1), expected, r
+
+
+def test_decode_mla_sink_reference_known_answer():
+    lat, q, bt, lens, scale, sinks, expected, r = mla_sink_case()
+    out = paged.decode_mla(q, lat, bt, lens, scale, kv_lora_rank=r, sinks=sinks)
+    assert np.all(np.isfinite(out))
+    np.testing.assert_allclose(out, expected, rtol=1e-12, atol=1e-12)
+
+
+def test_decode_mla_sink_equals_a_zero_value_token():
+    """Head h's sink s_h equals one more latent row with c_kv = 0 (a zero value) whose
+    score against head h is exactly s_h. With every head's q_pe = a_h u (one shared
+    direction u), the row k_pe = t u scores a_h t |u|^2 scale, so the sinks
+    s_h = a_h t |u|^2 scale are matched for all heads by that single row."""
+    rng = np.random.default_rng(11)
+    b, h, r, p, bs, scale = 4, 6, 32, 8, 16, 0.1
+    lens = np.array([0, 1, 30, 47], np.int32)
+    nblk = (int(lens.max()) + 1 + bs - 1) // bs
+    bt = np.arange(b * nblk, dtype=np.int32).reshape(b, nblk)
+    lat = rng.standard_normal((b * nblk, bs, r + p))
+    u = rng.standard_normal(p)
+    a = rng.standard_normal(h)
+    q = rng.standard_normal((b, h, r + p))
+    q[:, :, r:] = a[None, :, None] * u[None, None, :]
+    t = 1.7
+    sinks = a * t * float(u @ u) * scale
+    out = paged.decode_mla(q, lat, bt, lens, scale, kv_lora_rank=r, sinks=sinks)
+    lat2 = lat.copy()
+    for i in range(b):
+        pos = int(lens[i])
+        lat2[bt[i, pos // bs], pos % bs, :r] = 0.0
+        lat2[bt[i, pos // bs], pos % bs, r:] = t * u
+    ref = paged.decode_mla(q, lat2, bt, lens + 1, scale, kv_lora_rank=r)
+    np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+    assert np.all(out[0] == 0.0)  # no context: the sink takes everything
+
+
+def test_decode_mla_sink_closed_forms():
+    """-inf sinks change nothing; n identical latent rows under a sink s give
+    c_kv * n / (n + e^(s - c)), c the common score."""
+    rng = np.random.default_rng(12)
+    b, h, r, p, bs, scale = 3, 4, 16, 8, 16, 0.25
+    lens = np.array([5, 16, 31], np.int32)
+    bt = np.arange(b * 2, dtype=np.int32).reshape(b, 2)
+    lat = rng.standard_normal((b * 2, bs, r + p))
+    q = rng.standard_normal((b, h, r + p))
+    none = paged.decode_mla(q, lat, bt, lens, scale, kv_lora_rank=r)
+    np.testing.assert_array_equal(paged.decode_mla(q, lat, bt, lens, scale, kv_lora_rank=r,
+                                                   sinks=np.full(h, -np.inf)), none)
+    lat[:] = lat[0, 0]
+    sinks = np.array([-1.0, 0.0, 2.0, 5.0])
+    out = paged.decode_mla(q, lat, bt, lens, scale, kv_lora_rank=r, sinks=sinks)
+    for i in range(b):
+        for hh in range(h):
+            c = float(q[i, hh] @ lat[0, 0]) * scale
+            n = float(lens[i])
+            np.testing.assert_allclose(out[i, hh], lat[0, 0, :r] * n / (n + math.exp(sinks[hh] - c)), rtol=1e-12)

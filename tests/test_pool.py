@@ -134,10 +134,39 @@ def test_max_model_len_bounds_tables_and_admission():
     m.append_slots(["a", "b"])  # a: 39 tokens
     m.append_slots(["a", "b"])  # a: 40 tokens, at the limit
     before = (m.seq_len("a"), m.seq_len("b"), m.num_free_blocks)
-    with pytest.raises(ValueError, match="at max_model_len 40"):
+    with pytest.raises(ValueError, match="max_model_len is 40"):
         m.append_slots(["b", "a"])
     assert (m.seq_len("a"), m.seq_len("b"), m.num_free_blocks) == before  # refused before any change
     bt, lens = m.tables(["a", "b"])
     assert bt.shape == (2, 3) and lens.tolist() == [40, 7]
     with pytest.raises(ValueError, match="exceeds the pool"):
         KVPool(1, 2, 16, 2, 64, max_model_len=33, device="cpu")
+
+
+def test_read_policy_descriptors_and_step_choice():
+    """Each cache carries one descriptor per read policy (flags 0 / WKV_CACHE_SHARED_BLOCKS);
+    a pool's layers default to the shared-safe policy, a step over sequences that share no
+    block chooses the streaming one, and the default cannot be changed after construction
+    (the descriptors are built once)."""
+    from wavelet_amd import PagedKVCache, _lib
+
+    pool = KVPool(2, 64, 16, 2, 64, device="cpu")
+    c = pool.layers[0]
+    assert c.shared_blocks and c.descriptor().flags == _lib.CACHE_SHARED_BLOCKS
+    assert c.descriptor(False).flags == 0 and c.descriptor(True).flags == _lib.CACHE_SHARED_BLOCKS
+    assert c.descriptor(False).k == c.descriptor(True).k == c.k.data_ptr()
+    with pytest.raises(AttributeError):
+        c.shared_blocks = False
+    plain = PagedKVCache(8, 16, 2, 64, device="cpu")
+    assert not plain.shared_blocks and plain.descriptor().flags == 0
+    m = pool.blocks
+    m.allocate("a", np.arange(20))
+    m.allocate("b", np.arange(33) + 50)
+    assert not pool.decode_shares_blocks(["a", "b"])
+    m.fork("a", "a2")
+    assert pool.decode_shares_blocks(["b", "a2"])
+    for s in ("a", "a2", "b"):
+        m.free(s)
+    pool.sleep()
+    with pytest.raises(RuntimeError, match="asleep"):
+        c.descriptor(False)

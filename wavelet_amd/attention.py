@@ -108,6 +108,7 @@ def paged_decode_gqa(
     slot_mapping: torch.Tensor | None = None,
     seq_order: torch.Tensor | None = None,
     sinks: torch.Tensor | None = None,
+    shared_blocks: bool | None = None,
 ) -> torch.Tensor:
     """One decode step of GQA attention: ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` bf16.
 
@@ -122,7 +123,11 @@ def paged_decode_gqa(
     result is the same, bit for bit, in any order. ``sinks`` (fp32 ``[Hq]``,
     natural-log logits, ``-inf`` = none) adds one zero-value logit per query
     head to its softmax: the learned sink of the reference's sparse attention
-    (wavelet/trainer/models/deepseek_v4/attention.py:89-95).
+    (wavelet/trainer/models/deepseek_v4/attention.py:89-95). ``shared_blocks``
+    is this step's read policy (None = the cache's default): True when some
+    block is read by more than one sequence of the step (K/V reads then keep
+    it cached for the next reader), False to stream every block past the
+    caches (``KVPool.decode_shares_blocks`` decides it from the step's tables).
     """
     if not isinstance(cache, PagedKVCache):
         raise ValueError("cache must be a PagedKVCache")
@@ -160,7 +165,7 @@ def paged_decode_gqa(
             block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), batch, msl, float(scale),
             int(partition_size), ws.data_ptr(), ws.numel(), _order(seq_order, batch, dev))
     tail = tail + ((sinks.data_ptr(),) if sinks is not None else ()) + (_stream(dev),)
-    desc = ctypes.byref(cache.descriptor())
+    desc = ctypes.byref(cache.descriptor(shared_blocks))
     if fused:
         fn = lib.wkv_append_paged_decode_gqa_sinks if sinks is not None else lib.wkv_append_paged_decode_gqa
         rc = fn(desc, new_key.data_ptr(), new_key.stride(0), new_key.stride(1), new_value.data_ptr(),
@@ -359,13 +364,18 @@ def paged_decode_mla(
     new_kv_c: torch.Tensor | None = None,
     new_k_pe: torch.Tensor | None = None,
     slot_mapping: torch.Tensor | None = None,
+    sinks: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Weight-absorbed MLA decode: ``q_nope [B, H, R]``, ``q_pe [B, H, P]`` -> ``[B, H, R]`` bf16.
 
     With ``new_kv_c [B, R]``, ``new_k_pe [B, P]`` and ``slot_mapping [B]`` the
     step's latent append is fused into the same launch: token ``b`` is written
     at ``slot_mapping[b]`` (position ``seq_lens[b] - 1`` of sequence ``b``) and
-    attended -- the same result as ``cache.append`` then this call.
+    attended -- the same result as ``cache.append`` then this call. ``sinks``
+    (fp32 ``[H]``, natural-log logits, ``-inf`` = none) adds one zero-value
+    logit per head to its softmax: the learned per-head sink of the
+    reference's shared-KV attention (wavelet/trainer/models/deepseek_v4/
+    attention.py:703, consumed at :89-95 and :763).
     """
     if not isinstance(cache, MLALatentCache):
         raise ValueError("cache must be an MLALatentCache")
@@ -393,6 +403,7 @@ def paged_decode_mla(
             rows.append(x)
         new_kv_c, new_k_pe = rows
         slot_mapping = _slots(slot_mapping, batch, dev)
+    sinks = _sinks(sinks, heads, dev)
     if out is None:
         out = torch.empty((batch, heads, cache.kv_lora_rank), dtype=torch.bfloat16, device=dev)
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != (batch, heads, cache.kv_lora_rank) or not out.is_contiguous():
@@ -407,12 +418,14 @@ def paged_decode_mla(
     ws = _workspace(dev, need)
     tail = (q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1), q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
             out.data_ptr(), heads, block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
-            seq_lens.data_ptr(), batch, msl, float(scale), int(partition_size), ws.data_ptr(), ws.numel(), _stream(dev))
+            seq_lens.data_ptr(), batch, msl, float(scale), int(partition_size), ws.data_ptr(), ws.numel())
+    tail = tail + ((sinks.data_ptr(),) if sinks is not None else ()) + (_stream(dev),)
     if fused:
-        rc = lib.wkv_append_paged_decode_mla(
-            ctypes.byref(cache.descriptor()), new_kv_c.data_ptr(), new_kv_c.stride(0), new_k_pe.data_ptr(),
-            new_k_pe.stride(0), slot_mapping.data_ptr(), *tail)
+        fn = lib.wkv_append_paged_decode_mla_sinks if sinks is not None else lib.wkv_append_paged_decode_mla
+        rc = fn(ctypes.byref(cache.descriptor()), new_kv_c.data_ptr(), new_kv_c.stride(0), new_k_pe.data_ptr(),
+                new_k_pe.stride(0), slot_mapping.data_ptr(), *tail)
     else:
-        rc = lib.wkv_paged_decode_mla(ctypes.byref(cache.descriptor()), *tail)
+        fn = lib.wkv_paged_decode_mla_sinks if sinks is not None else lib.wkv_paged_decode_mla
+        rc = fn(ctypes.byref(cache.descriptor()), *tail)
     _lib.check(rc, "paged_decode_mla")
     return out

@@ -180,37 +180,82 @@ class BlockManager:
                 self._ref[b] += 1
             self._seqs[dst] = _Seq(blocks=list(src.blocks[:n]), length=length)
 
-    def append_slots(self, seq_ids) -> tuple[np.ndarray, list[tuple[int, int]]]:
-        """Reserve one new token slot per sequence (a decode step).
+    def _append_plan(self, seq_ids, num_tokens: int) -> int:
+        """New blocks ``append_slots(seq_ids, num_tokens)`` would take (fresh blocks and
+        copy-on-write copies), counted without changing any state; raises ValueError for a
+        sequence listed twice or one that would pass ``max_model_len``."""
+        if num_tokens < 0:
+            raise ValueError(f"num_tokens must be non-negative (got {num_tokens})")
+        if len(set(seq_ids)) != len(seq_ids):
+            raise ValueError("a sequence is listed twice")
+        bs = self.block_size
+        released: dict[int, int] = {}  # block -> references the plan has already moved off it
+        need = 0
+        for sid in seq_ids:
+            seq = self._seqs[sid]
+            if self.max_model_len is not None and seq.length + num_tokens > self.max_model_len:
+                raise ValueError(f"sequence {sid!r} at {seq.length} tokens cannot take {num_tokens} more: "
+                                 f"max_model_len is {self.max_model_len}")
+            if num_tokens == 0:
+                continue
+            pos = seq.length
+            if pos < len(seq.blocks) * bs:  # the first token lands in an existing, partly filled block
+                last = seq.blocks[pos // bs]
+                if self._ref[last] - released.get(last, 0) > 1:
+                    need += 1
+                    released[last] = released.get(last, 0) + 1
+            need += max(-(-(pos + num_tokens) // bs) - len(seq.blocks), 0)
+        return need
 
-        Returns the int64 slot of each sequence's new token and the
-        copy-on-write pairs ``(src_block, dst_block)`` to apply with
-        ``PagedKVCache.copy_blocks`` on every layer *before* the append: a
-        sequence about to write into a block it still shares gets a private
-        copy first.
+    def append_slots(self, seq_ids, num_tokens: int = 1) -> tuple[np.ndarray, list[tuple[int, int]]]:
+        """Reserve ``num_tokens`` new token slots per sequence (a decode step: one).
+
+        Returns the int64 slots, sequence-major (``[len(seq_ids) * num_tokens]``:
+        sequence ``i``'s tokens at ``i * num_tokens ..``), and the copy-on-write
+        pairs ``(src_block, dst_block)`` to apply with ``copy_blocks`` on every
+        layer (``KVPool.copy_blocks``) *before* the append: a sequence about to
+        write into a block it still shares gets a private copy first. Nothing
+        changes unless every sequence can take its tokens: one that would pass
+        ``max_model_len`` raises ValueError, and a step needing more blocks than
+        are free raises MemoryError, before any state moves.
         """
-        if self.max_model_len is not None:
-            for sid in seq_ids:  # checked before any state changes
-                if self._seqs[sid].length >= self.max_model_len:
-                    raise ValueError(f"sequence {sid!r} is at max_model_len {self.max_model_len}: no further token")
-        slots = np.empty(len(seq_ids), dtype=np.int64)
+        seq_ids = list(seq_ids)
+        need = self._append_plan(seq_ids, int(num_tokens))
+        if need > self.num_free_blocks:
+            raise MemoryError(f"out of KV cache blocks: the step needs {need}, {self.num_free_blocks} are free")
+        slots = np.empty(len(seq_ids) * num_tokens, dtype=np.int64)
         cow: list[tuple[int, int]] = []
         bs = self.block_size
         for i, sid in enumerate(seq_ids):
             seq = self._seqs[sid]
-            pos = seq.length
-            if pos == len(seq.blocks) * bs:
-                seq.blocks.append(self._take())
-            else:
-                last = seq.blocks[pos // bs]
-                if self._ref[last] > 1:  # a partially filled block still shared with the group
-                    fresh = self._take()
-                    cow.append((last, fresh))
-                    self._release(last)
-                    seq.blocks[pos // bs] = fresh
-            slots[i] = seq.blocks[pos // bs] * bs + pos % bs
-            seq.length += 1
+            for t in range(num_tokens):
+                pos = seq.length
+                if pos == len(seq.blocks) * bs:
+                    seq.blocks.append(self._take())
+                else:
+                    last = seq.blocks[pos // bs]
+                    if self._ref[last] > 1:  # a partially filled block still shared with the group
+                        fresh = self._take()
+                        cow.append((last, fresh))
+                        self._release(last)
+                        seq.blocks[pos // bs] = fresh
+                slots[i * num_tokens + t] = seq.blocks[pos // bs] * bs + pos % bs
+                seq.length += 1
         return slots, cow
+
+    def blocks_needed(self, seq_ids, num_tokens: int = 1) -> int:
+        """Blocks ``append_slots(seq_ids, num_tokens)`` would take from the free pool."""
+        return self._append_plan(list(seq_ids), int(num_tokens))
+
+    def any_shared(self, seq_ids) -> bool:
+        """Whether any block of these sequences is held by more than one sequence: a
+        decode step over them then reads such blocks more than once, and should keep
+        them cached (the decode's read policy, ``shared_blocks``)."""
+        for sid in seq_ids:
+            blocks = self._seqs[sid].blocks
+            if blocks and int(self._ref[np.asarray(blocks, dtype=np.int64)].max()) > 1:
+                return True
+        return False
 
     def free(self, seq_id) -> None:
         """Release a finished sequence's blocks (indexed prompt blocks stay matchable)."""

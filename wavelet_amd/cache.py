@@ -79,8 +79,7 @@ class PagedKVCache:
         if num_blocks <= 0 or num_kv_heads <= 0:
             raise ValueError("num_blocks and num_kv_heads must be positive")
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-        # blocks read by several sequences (prefix caching): reads keep them cached
-        self.shared_blocks = bool(shared_blocks)
+        self._shared_blocks = bool(shared_blocks)
         self.num_blocks = int(num_blocks)
         self.block_size = int(block_size)
         self.num_kv_heads = int(num_kv_heads)
@@ -97,18 +96,23 @@ class PagedKVCache:
         self.v = torch.zeros((nb, h, d, bs), dtype=elem, device=self.device)
         self.k_scale = torch.zeros((nb, h), dtype=torch.float32, device=self.device) if fp8 else None
         self.v_scale = torch.zeros((nb, h), dtype=torch.float32, device=self.device) if fp8 else None
-        self._desc = _lib.WkvCache(
-            k=self.k.data_ptr(),
-            v=self.v.data_ptr(),
-            k_scale=self.k_scale.data_ptr() if fp8 else None,
-            v_scale=self.v_scale.data_ptr() if fp8 else None,
-            num_blocks=self.num_blocks,
-            block_size=self.block_size,
-            num_kv_heads=self.num_kv_heads,
-            head_dim=self.head_dim,
-            kv_dtype=KV_DTYPES[self.kv_dtype],
-            flags=_lib.CACHE_SHARED_BLOCKS if self.shared_blocks else 0,
-        )
+        # one descriptor per read policy (the flag is read per call); _desc is the default one
+        self._descs = {
+            shared: _lib.WkvCache(
+                k=self.k.data_ptr(),
+                v=self.v.data_ptr(),
+                k_scale=self.k_scale.data_ptr() if fp8 else None,
+                v_scale=self.v_scale.data_ptr() if fp8 else None,
+                num_blocks=self.num_blocks,
+                block_size=self.block_size,
+                num_kv_heads=self.num_kv_heads,
+                head_dim=self.head_dim,
+                kv_dtype=KV_DTYPES[self.kv_dtype],
+                flags=_lib.CACHE_SHARED_BLOCKS if shared else 0,
+            )
+            for shared in (False, True)
+        }
+        self._desc = self._descs[self._shared_blocks]
 
     # -- sleep / wake (the engine's sleep(level=1) / wake_up(tags=["kv_cache"]),
     #    wavelet/inference/engine.py:858-873) ---------------------------------
@@ -120,6 +124,7 @@ class PagedKVCache:
         """Release the pool's device memory; the contents are discarded."""
         self.k = self.v = self.k_scale = self.v_scale = None
         self._desc = None
+        self._descs = None
 
     def wake_up(self) -> None:
         """Allocate the pool again (zeroed); a no-op when awake."""
@@ -141,10 +146,20 @@ class PagedKVCache:
             n += 2 * self.num_blocks * self.num_kv_heads * 4
         return n
 
-    def descriptor(self) -> ctypes.Structure:
+    @property
+    def shared_blocks(self) -> bool:
+        """The decodes' default read policy (fixed at construction; a call can choose per
+        step): True when several sequences may read one block (prefix caching, forks) --
+        K/V reads then keep blocks cached for the next reader; False streams them past the
+        caches as read-once data (3-9% faster when nothing is shared)."""
+        return self._shared_blocks
+
+    def descriptor(self, shared_blocks: bool | None = None) -> ctypes.Structure:
+        """The C descriptor of this cache, with the read policy ``shared_blocks`` (None =
+        the cache's default)."""
         if self._desc is None:
             raise RuntimeError("the KV cache is asleep: call wake_up() first")
-        return self._desc
+        return self._desc if shared_blocks is None else self._descs[bool(shared_blocks)]
 
     # -- operations ---------------------------------------------------------
     def append(self, key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor) -> None:
@@ -290,6 +305,37 @@ class MLALatentCache:
             slots.data_ptr(), n, _stream(self.device),
         )
         _lib.check(rc, "mla_append")
+
+    def gather(self, block_table: torch.Tensor, seq_lens: torch.Tensor, *,
+               total_tokens: int | None = None) -> torch.Tensor:
+        """Contiguous ``[sum(seq_lens), kv_lora_rank + rope_dim]`` bf16 copy of every
+        sequence's latent rows (``c_kv`` then ``k_pe``), in sequence order: the
+        cached-context read of an MLA chunked prefill or prefix-cache hit."""
+        block_table, seq_lens = check_tables(block_table, seq_lens, self.device, self.block_size)
+        batch = seq_lens.shape[0]
+        cu = torch.zeros(batch, dtype=torch.int64, device=self.device)
+        if batch > 1:
+            cu[1:] = torch.cumsum(seq_lens[:-1].to(torch.int64), 0)
+        total = int(seq_lens.to(torch.int64).sum().item()) if total_tokens is None else int(total_tokens)
+        out = torch.empty((total, self.kv_lora_rank + self.rope_dim), dtype=torch.bfloat16, device=self.device)
+        if total == 0 or batch == 0:
+            return out
+        rc = _lib.load().wkv_mla_gather(
+            ctypes.byref(self.descriptor()), block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+            seq_lens.data_ptr(), cu.data_ptr(), batch, out.data_ptr(), _stream(self.device),
+        )
+        _lib.check(rc, "mla_gather")
+        return out
+
+    def copy_blocks(self, block_mapping: torch.Tensor) -> None:
+        """Copy latent block ``mapping[i, 0]`` onto ``mapping[i, 1]`` (copy-on-write)."""
+        _require_cuda(block_mapping, "block_mapping", self.device)
+        if block_mapping.dtype != torch.int64 or block_mapping.dim() != 2 or block_mapping.shape[1] != 2:
+            raise ValueError("block_mapping must be int64 [n, 2]")
+        m = block_mapping.contiguous()
+        rc = _lib.load().wkv_mla_copy_blocks(ctypes.byref(self.descriptor()), m.data_ptr(), m.shape[0],
+                                             _stream(self.device))
+        _lib.check(rc, "mla_copy_blocks")
 
 
 def check_tables(block_table: torch.Tensor, seq_lens: torch.Tensor, device: torch.device,

@@ -180,15 +180,23 @@ struct MlaAppend {
   const int64_t *slots;
 };
 
+// Weight of head h's attention sink in a denominator whose terms are
+// 2^(s - m_use) (log2 domain): one more logit, natural-log units like the
+// scaled scores, with a zero value vector
+// (wavelet/trainer/models/deepseek_v4/attention.py:89-95). No sinks: 0.
+__device__ __forceinline__ float mla_sink_weight(const float *sinks, int h, float m_use) {
+  return sinks != nullptr ? exp2f(sinks[h] * 1.4426950408889634f - m_use) : 0.f;
+}
+
 // Log-sum-exp merge of the per-partition partials of one (sequence, head):
 // 128 lanes per head, four output elements (one 8-byte partial load per
 // partition) per lane, two heads per 256-thread workgroup. A partial is the
 // partition's normalised output o_p (bf16) with its maximum m_p and sum l_p:
-// out = sum_p 2^(m_p - M) l_p o_p / sum_p 2^(m_p - M) l_p.
+// out = sum_p 2^(m_p - M) l_p o_p / (sum_p 2^(m_p - M) l_p + sink weight).
 __global__ __launch_bounds__(256) void mla_merge_kernel(const uint16_t *__restrict__ part_o,
                                                         const float *__restrict__ part_ml, uint16_t *__restrict__ out,
                                                         const int32_t *__restrict__ seq_lens, int max_seq, int H,
-                                                        int P_tok, int max_parts) {
+                                                        int P_tok, int max_parts, const float *__restrict__ sinks) {
   constexpr int R = mla::R;
   const int h = 2 * blockIdx.x + (threadIdx.x >> 7), b = blockIdx.y, d = 4 * (threadIdx.x & 127);
   if (h >= H) return;
@@ -209,6 +217,7 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(const uint16_t *__restri
 #pragma unroll
     for (int i = 0; i < 4; ++i) num[i] += wl * __uint_as_float((o[i >> 1] >> (16 * (i & 1))) << 16);
   }
+  den += mla_sink_weight(sinks, h, m_use);
   const float inv = den > 0.f ? 1.f / den : 0.f;
   u32x2 v;
   v[0] = f32_to_bf16_bits(num[0] * inv) | (f32_to_bf16_bits(num[1] * inv) << 16);
@@ -252,7 +261,7 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     const uint16_t *__restrict__ qp, int64_t qp_sb, int64_t qp_sh, uint16_t *__restrict__ out,
     uint16_t *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
     int Mb, int max_seq, const int32_t *__restrict__ seq_lens, int BS, int64_t NB, float scale_log2, int P_tok,
-    int max_parts, int H, int batch, MlaAppend ap, int seq_xcd) {
+    int max_parts, int H, int batch, MlaAppend ap, int seq_xcd, const float *__restrict__ sinks) {
   using namespace mla;
   constexpr int NHB = NQ;           // 16-head blocks of this workgroup
   constexpr int HW = 16 * NHB;      // heads of this workgroup
@@ -499,7 +508,10 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     for (int c = 0; c < NHB; ++c) {
       const int hl = 16 * c + col, h = hbase + hl;
       const float lh = lsum_s[hl];
-      const float inv = lh > 0.f ? 1.f / lh : 0.f;
+      // A whole sequence in one partition is finished here, sink included;
+      // a partial carries (m, l) and the merge adds the sink.
+      const float den = nparts == 1 ? lh + mla_sink_weight(sinks, h, mrun_s[hl] == -INFINITY ? 0.f : mrun_s[hl]) : lh;
+      const float inv = den > 0.f ? 1.f / den : 0.f;
       uint16_t *dst = nparts == 1 ? out + (static_cast<int64_t>(b) * H + h) * R
                                   : part_o + ((static_cast<int64_t>(b) * H + h) * max_parts + part) * R;
 #pragma unroll
@@ -685,7 +697,7 @@ static int launch_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t 
                       const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
                       const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
                       int32_t partition_size, void *workspace, int64_t workspace_bytes, const MlaAppend &ap,
-                      void *stream) {
+                      const float *sinks, void *stream) {
   WKV_CHECK_ARG(cache != nullptr && cache->latent != nullptr && aligned16(cache->latent), "bad MLA cache");
   WKV_CHECK_ARG(cache->num_blocks > 0 && cache->num_blocks <= 0x7fffffff && cache->block_size > 0 &&
                     cache->block_size % 16 == 0 && cache->block_size <= 256,
@@ -737,7 +749,7 @@ static int launch_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t 
                                                     qp_stride_h, oo, part_o, part_ml, block_table, bt_stride,      \
                                                     max_blocks_per_seq, max_seq, seq_lens, BS, cache->num_blocks, \
                                                     scale_log2, partition_size, max_parts, num_heads, batch, ap,  \
-                                                    batch % 8 == 0)
+                                                    batch % 8 == 0, sinks)
   switch (num_heads) {
     case 16: WKV_MLA(1); break;
     case 32: WKV_MLA(2); break;
@@ -747,7 +759,7 @@ static int launch_mla(const wkv_mla_cache_t *cache, const void *q_nope, int64_t 
   WKV_CHECK_LAUNCH("wkv_paged_decode_mla");
   if (max_parts > 1) {
     mla_merge_kernel<<<dim3(static_cast<unsigned>((num_heads + 1) / 2), static_cast<unsigned>(batch)), 256, 0, s>>>(
-        part_o, part_ml, oo, seq_lens, max_seq, num_heads, partition_size, max_parts);
+        part_o, part_ml, oo, seq_lens, max_seq, num_heads, partition_size, max_parts, sinks);
     WKV_CHECK_LAUNCH("wkv_paged_decode_mla merge");
   }
   return WKV_OK;
@@ -764,7 +776,21 @@ extern "C" int wkv_paged_decode_mla(const wkv_mla_cache_t *cache, const void *q_
   const MlaAppend none{nullptr, 0, nullptr, 0, nullptr};
   return launch_mla(cache, q_nope, qn_stride_b, qn_stride_h, q_pe, qp_stride_b, qp_stride_h, out, num_heads,
                     block_table, bt_stride, max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size,
-                    workspace, workspace_bytes, none, stream);
+                    workspace, workspace_bytes, none, nullptr, stream);
+}
+
+extern "C" int wkv_paged_decode_mla_sinks(const wkv_mla_cache_t *cache, const void *q_nope, int64_t qn_stride_b,
+                                          int64_t qn_stride_h, const void *q_pe, int64_t qp_stride_b,
+                                          int64_t qp_stride_h, void *out, int32_t num_heads,
+                                          const int32_t *block_table, int64_t bt_stride, int32_t max_blocks_per_seq,
+                                          const int32_t *seq_lens, int32_t batch, int32_t max_seq_len, float scale,
+                                          int32_t partition_size, void *workspace, int64_t workspace_bytes,
+                                          const float *sinks, void *stream) {
+  WKV_CHECK_ARG(sinks != nullptr && reinterpret_cast<uintptr_t>(sinks) % 4 == 0, "sinks must be non-NULL fp32");
+  const MlaAppend none{nullptr, 0, nullptr, 0, nullptr};
+  return launch_mla(cache, q_nope, qn_stride_b, qn_stride_h, q_pe, qp_stride_b, qp_stride_h, out, num_heads,
+                    block_table, bt_stride, max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size,
+                    workspace, workspace_bytes, none, sinks, stream);
 }
 
 extern "C" int wkv_append_paged_decode_mla(const wkv_mla_cache_t *cache, const void *kv_c, int64_t kv_c_stride,
@@ -783,5 +809,27 @@ extern "C" int wkv_append_paged_decode_mla(const wkv_mla_cache_t *cache, const v
                      k_pe_stride, slot_mapping};
   return launch_mla(cache, q_nope, qn_stride_b, qn_stride_h, q_pe, qp_stride_b, qp_stride_h, out, num_heads,
                     block_table, bt_stride, max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size,
-                    workspace, workspace_bytes, ap, stream);
+                    workspace, workspace_bytes, ap, nullptr, stream);
+}
+
+extern "C" int wkv_append_paged_decode_mla_sinks(const wkv_mla_cache_t *cache, const void *kv_c,
+                                                 int64_t kv_c_stride, const void *k_pe, int64_t k_pe_stride,
+                                                 const int64_t *slot_mapping, const void *q_nope,
+                                                 int64_t qn_stride_b, int64_t qn_stride_h, const void *q_pe,
+                                                 int64_t qp_stride_b, int64_t qp_stride_h, void *out,
+                                                 int32_t num_heads, const int32_t *block_table, int64_t bt_stride,
+                                                 int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
+                                                 int32_t max_seq_len, float scale, int32_t partition_size,
+                                                 void *workspace, int64_t workspace_bytes, const float *sinks,
+                                                 void *stream) {
+  WKV_CHECK_ARG(sinks != nullptr && reinterpret_cast<uintptr_t>(sinks) % 4 == 0, "sinks must be non-NULL fp32");
+  WKV_CHECK_ARG(kv_c && k_pe && aligned16(kv_c) && aligned16(k_pe), "kv_c/k_pe must be non-NULL and 16-byte aligned");
+  WKV_CHECK_ARG(kv_c_stride >= 0 && k_pe_stride >= 0 && (kv_c_stride | k_pe_stride) % 8 == 0,
+                "kv_c/k_pe row strides must be non-negative multiples of 8");
+  WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+  const MlaAppend ap{static_cast<const uint16_t *>(kv_c), kv_c_stride, static_cast<const uint16_t *>(k_pe),
+                     k_pe_stride, slot_mapping};
+  return launch_mla(cache, q_nope, qn_stride_b, qn_stride_h, q_pe, qp_stride_b, qp_stride_h, out, num_heads,
+                    block_table, bt_stride, max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size,
+                    workspace, workspace_bytes, ap, sinks, stream);
 }

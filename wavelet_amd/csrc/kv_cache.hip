@@ -319,6 +319,41 @@ __global__ __launch_bounds__(256) void mla_append_kernel(uint16_t *__restrict__ 
   *reinterpret_cast<u32x4 *>(lat + slot * W + c * 8) = *reinterpret_cast<const u32x4 *>(src);
 }
 
+// ---------------------------------------------------------------------------
+// MLA latent gather: one workgroup per (block j of sequence i). A block's
+// rows are one contiguous run of BS rows in the cache, and the rows a
+// sequence takes from it are one contiguous run of the output: a plain
+// 16-byte copy of ntok * row_bytes.
+__global__ __launch_bounds__(256) void mla_gather_kernel(const uint8_t *__restrict__ lat,
+                                                         const int32_t *__restrict__ bt, int64_t bt_stride, int Mb,
+                                                         const int32_t *__restrict__ seq_lens,
+                                                         const int64_t *__restrict__ cu, uint8_t *__restrict__ out,
+                                                         int row_bytes, int BS, int64_t NB) {
+  const int i = blockIdx.y, j = blockIdx.x;
+  int L = seq_lens[i];
+  L = L < Mb * BS ? L : Mb * BS;
+  if (L <= 0 || j * BS >= L) return;
+  const int64_t blk = bt[i * bt_stride + j];
+  if (blk < 0 || blk >= NB) return;
+  const int ntok = (L - j * BS) < BS ? (L - j * BS) : BS;
+  const int n16 = ntok * (row_bytes / 16);
+  const u32x4 *src = reinterpret_cast<const u32x4 *>(lat + blk * BS * static_cast<int64_t>(row_bytes));
+  u32x4 *dst = reinterpret_cast<u32x4 *>(out + (cu[i] + static_cast<int64_t>(j) * BS) * row_bytes);
+  for (int w = threadIdx.x; w < n16; w += 256) dst[w] = src[w];
+}
+
+// Whole-block copy of an MLA latent cache: one workgroup per (src, dst) pair.
+__global__ __launch_bounds__(256) void mla_copy_blocks_kernel(uint8_t *__restrict__ lat,
+                                                              const int64_t *__restrict__ mapping,
+                                                              int64_t block_bytes, int64_t NB) {
+  const int64_t src = mapping[2 * blockIdx.x], dst = mapping[2 * blockIdx.x + 1];
+  if (src < 0 || dst < 0 || src >= NB || dst >= NB) return;
+  const int64_t n16 = block_bytes / 16;
+  const u32x4 *s4 = reinterpret_cast<const u32x4 *>(lat + src * block_bytes);
+  u32x4 *d4 = reinterpret_cast<u32x4 *>(lat + dst * block_bytes);
+  for (int64_t w = threadIdx.x; w < n16; w += 256) d4[w] = s4[w];
+}
+
 static int check_kv_input(const void *p, int64_t st_t, int64_t st_h, const char *name) {
   WKV_CHECK_ARG(p != nullptr, "%s is NULL", name);
   WKV_CHECK_ARG(aligned16(p), "%s must be 16-byte aligned", name);
@@ -420,17 +455,11 @@ extern "C" int wkv_append_fp8(const wkv_cache_t *cache, const void *key, int64_t
 extern "C" int wkv_mla_append(const wkv_mla_cache_t *cache, const void *kv_c, int64_t kv_c_stride,
                               const void *k_pe, int64_t k_pe_stride, const int64_t *slot_mapping,
                               int64_t num_tokens, void *stream) {
-  WKV_CHECK_ARG(cache != nullptr && cache->latent != nullptr, "MLA cache is NULL");
-  WKV_CHECK_ARG(aligned16(cache->latent), "MLA latent cache must be 16-byte aligned");
-  WKV_CHECK_ARG(cache->num_blocks > 0 && cache->block_size > 0 && cache->block_size % 16 == 0,
-                "bad MLA cache geometry");
-  WKV_CHECK_ARG(cache->kv_lora_rank % 8 == 0 && cache->rope_dim % 8 == 0 && cache->kv_lora_rank > 0 &&
-                    cache->rope_dim >= 0,
-                "kv_lora_rank and rope_dim must be multiples of 8");
+  int rc = check_mla_cache(cache);
+  if (rc) return rc;
   WKV_CHECK_ARG(num_tokens >= 0, "num_tokens must be >= 0");
   if (num_tokens == 0) return WKV_OK;
   WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
-  int rc;
   if ((rc = check_kv_input(kv_c, kv_c_stride, 0, "kv_c"))) return rc;
   if (cache->rope_dim > 0 && (rc = check_kv_input(k_pe, k_pe_stride, 0, "k_pe"))) return rc;
   const int C = (cache->kv_lora_rank + cache->rope_dim) / 8;
@@ -496,5 +525,39 @@ extern "C" int wkv_copy_blocks(const wkv_cache_t *cache, const int64_t *block_ma
       static_cast<uint8_t *>(cache->k), static_cast<uint8_t *>(cache->v), fp8 ? cache->k_scale : nullptr,
       fp8 ? cache->v_scale : nullptr, block_mapping, block_bytes, cache->num_kv_heads, cache->num_blocks);
   WKV_CHECK_LAUNCH("wkv_copy_blocks");
+  return WKV_OK;
+}
+
+extern "C" int wkv_mla_gather(const wkv_mla_cache_t *cache, const int32_t *block_table, int64_t bt_stride,
+                              int32_t max_blocks_per_seq, const int32_t *seq_lens, const int64_t *cu_seq_lens,
+                              int32_t batch, void *out, void *stream) {
+  int rc = check_mla_cache(cache);
+  if (rc) return rc;
+  WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535]");
+  if (batch == 0 || max_blocks_per_seq == 0) return WKV_OK;
+  WKV_CHECK_ARG(max_blocks_per_seq > 0 && bt_stride >= max_blocks_per_seq, "bad block table geometry");
+  WKV_CHECK_ARG(block_table && seq_lens && cu_seq_lens, "block_table / seq_lens / cu_seq_lens is NULL");
+  WKV_CHECK_ARG(out != nullptr && aligned16(out), "out must be non-NULL and 16-byte aligned");
+  const int row_bytes = 2 * (cache->kv_lora_rank + cache->rope_dim);
+  const dim3 grid(static_cast<unsigned>(max_blocks_per_seq), static_cast<unsigned>(batch));
+  mla_gather_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint8_t *>(cache->latent), block_table, bt_stride, max_blocks_per_seq, seq_lens, cu_seq_lens,
+      static_cast<uint8_t *>(out), row_bytes, cache->block_size, cache->num_blocks);
+  WKV_CHECK_LAUNCH("wkv_mla_gather");
+  return WKV_OK;
+}
+
+extern "C" int wkv_mla_copy_blocks(const wkv_mla_cache_t *cache, const int64_t *block_mapping, int64_t n,
+                                   void *stream) {
+  int rc = check_mla_cache(cache);
+  if (rc) return rc;
+  WKV_CHECK_ARG(n >= 0 && n < (1ll << 31), "n out of range");
+  if (n == 0) return WKV_OK;
+  WKV_CHECK_ARG(block_mapping != nullptr, "block_mapping is NULL");
+  const int64_t block_bytes =
+      static_cast<int64_t>(cache->block_size) * (cache->kv_lora_rank + cache->rope_dim) * 2;
+  mla_copy_blocks_kernel<<<dim3(static_cast<unsigned>(n)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<uint8_t *>(cache->latent), block_mapping, block_bytes, cache->num_blocks);
+  WKV_CHECK_LAUNCH("wkv_mla_copy_blocks");
   return WKV_OK;
 }

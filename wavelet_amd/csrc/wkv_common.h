@@ -44,6 +44,7 @@ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Validates the parts of a cache descriptor every entry point relies on.
 // want_dtype: a wkv_kv_dtype_t the entry point requires, or -1 for either.
 int check_cache(const wkv_cache_t *c, int want_dtype);
+int check_mla_cache(const wkv_mla_cache_t *c);
 
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32 (bit level, RNE, NaN kept quiet) — matches torch's conversion.

@@ -79,7 +79,9 @@ class PagedCache(Cache):
 
     Each model step reserves the step's token slots once (its first layer's ``update``), applies
     the block manager's copy-on-write pairs to every layer, and hands every layer the same
-    block table, lengths and slot mapping. Use with ``attn_implementation="wavelet_paged"``.
+    block table, lengths and slot mapping; the step's decodes keep K/V cached only when some
+    block is held by more than one row (``BlockManager.any_shared``), else they stream it.
+    Use with ``attn_implementation="wavelet_paged"``.
     """
 
     def __init__(self, pool: KVPool, seq_ids) -> None:
@@ -101,25 +103,28 @@ class PagedCache(Cache):
             raise RuntimeError(f"layers {sorted(self._pending)} were updated but never attended: the attention "
                                f"implementation must be {ATTN_IMPLEMENTATION!r}")
         bm, bs = self.pool.blocks, self.pool.block_size
-        slots = np.empty((len(self.seq_ids), tokens), dtype=np.int64)
-        cow: list[tuple[int, int]] = []
-        for i, sid in enumerate(self.seq_ids):
-            if sid not in bm:
-                # a new sequence: its prompt's blocks (token ids unseen here, so a private salt
-                # keeps the prefix index from matching them)
-                bm.allocate(sid, np.zeros(tokens, dtype=np.int64), cache_salt=f"{self._salt}-{sid}")
-                blocks = bm.blocks_of(sid)
-                pos = np.arange(tokens)
-                slots[i] = np.asarray(blocks, dtype=np.int64)[pos // bs] * bs + pos % bs
-            else:
-                for t in range(tokens):
-                    s, pairs = bm.append_slots([sid])
-                    slots[i, t] = s[0]
-                    cow.extend(pairs)
-        if cow:  # a row about to write into a block it still shares gets its own copy first
-            pairs = torch.tensor(cow, dtype=torch.int64, device=device)
-            for layer in self.pool.layers:
-                layer.copy_blocks(pairs)
+        old_rows = [sid for sid in self.seq_ids if sid in bm]
+        new_rows = [sid for sid in self.seq_ids if sid not in bm]
+        # every check before any state moves: a step that cannot be taken leaves the manager as it was
+        if new_rows and bm.max_model_len is not None and tokens > bm.max_model_len:
+            raise ValueError(f"a new sequence of {tokens} tokens is longer than max_model_len {bm.max_model_len}")
+        need = bm.blocks_needed(old_rows, tokens) + len(new_rows) * -(-tokens // bs)
+        if need > bm.num_free_blocks:
+            raise MemoryError(f"out of KV cache blocks: the step needs {need}, {bm.num_free_blocks} are free")
+        rows: dict = {}
+        if old_rows:
+            s, cow = bm.append_slots(old_rows, tokens)
+            for i, sid in enumerate(old_rows):
+                rows[sid] = s[i * tokens:(i + 1) * tokens]
+            # a row about to write into a block it still shares gets its own copy first
+            self.pool.copy_blocks(cow)
+        pos = np.arange(tokens)
+        for sid in new_rows:
+            # a new sequence: its prompt's blocks (token ids unseen here, so a private salt
+            # keeps the prefix index from matching them)
+            bm.allocate(sid, np.zeros(tokens, dtype=np.int64), cache_salt=f"{self._salt}-{sid}")
+            rows[sid] = np.asarray(bm.blocks_of(sid), dtype=np.int64)[pos // bs] * bs + pos % bs
+        slots = np.stack([rows[sid] for sid in self.seq_ids])
         bt, sl = bm.tables(self.seq_ids)
         self._step = {
             "tokens": tokens,
@@ -128,6 +133,8 @@ class PagedCache(Cache):
             "seq_lens": torch.from_numpy(sl).to(device),
             "cu_seqlens_q": torch.arange(0, len(self.seq_ids) * tokens + 1, tokens, dtype=torch.int32, device=device),
             "max_seq_len": int(sl.max()),
+            # blocks held by more than one row are read more than once: keep them cached
+            "shared_blocks": bm.any_shared(self.seq_ids),
         }
         self._staged.clear()
 
@@ -159,7 +166,8 @@ class PagedCache(Cache):
         cache = self.pool.layers[layer]
         if tokens == 1:
             out = paged_decode_gqa(q, cache, st["block_table"], st["seq_lens"], scale, max_seq_len=st["max_seq_len"],
-                                   new_key=kk, new_value=vv, slot_mapping=st["slots"], sinks=sinks)
+                                   new_key=kk, new_value=vv, slot_mapping=st["slots"], sinks=sinks,
+                                   shared_blocks=st["shared_blocks"])
         else:
             out = prefill_gqa(q, cache, st["block_table"], st["seq_lens"], st["cu_seqlens_q"], scale, key=kk,
                               value=vv, slot_mapping=st["slots"], max_query_len=tokens,

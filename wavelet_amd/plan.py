@@ -22,7 +22,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import _workspace
+from .attention import _workspace, decode_plan
 from .cache import PagedKVCache, _require_cuda, check_tables
 
 
@@ -63,8 +63,9 @@ class _Live:
 class _LayerCall:
     append_fn: object
     append_args: tuple
-    decode_args: tuple
-    fused_args: tuple
+    decode_args: dict  # read policy (shared_blocks) -> the attention call's arguments
+    fused_args: dict   # read policy -> the fused append + attention call's arguments
+    shared_default: bool
 
 
 class DecodeStep:
@@ -91,6 +92,13 @@ class DecodeStep:
     costs more than mixed lengths lose. Calling ``step_layer`` / ``attend``
     directly uses the order of the last ``prepare`` (the batch order before
     the first).
+
+    ``run``, ``attend`` and ``step_layer`` take the step's read policy
+    ``shared_blocks`` (None = each cache's default): True when some block of
+    the step is read by more than one sequence (K/V reads keep it cached for
+    the next reader), False to stream every block (``KVPool.decode_shares_blocks``
+    computes it from the block manager's reference counts once per step). The
+    group-aware decode chooses its own policy per role.
     """
 
     def __init__(self, caches: list[PagedKVCache], q: list[torch.Tensor], key: list[torch.Tensor],
@@ -141,26 +149,30 @@ class DecodeStep:
                 if t.dtype != torch.bfloat16 or tuple(t.shape) != shape or not t.is_contiguous() or t.device != dev:
                     raise ValueError(f"layer {layer}: {name} must be a contiguous bfloat16 {shape} tensor on {dev}")
             fn = lib.wkv_append_fp8 if cache.kv_dtype == "fp8_e4m3" else lib.wkv_append
-            desc = ctypes.byref(cache.descriptor())
-            append_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
-                           vv.stride(1), slot_mapping.data_ptr(), slot_mapping.numel(), self.stream)
+            append_args = (ctypes.byref(cache.descriptor()), kk.data_ptr(), kk.stride(0), kk.stride(1),
+                           vv.data_ptr(), vv.stride(0), vv.stride(1), slot_mapping.data_ptr(), slot_mapping.numel(),
+                           self.stream)
             tail = (qq.data_ptr(), qq.stride(0), qq.stride(1), oo.data_ptr(), hq,
                     self.block_table.data_ptr(), self.block_table.stride(0), self.block_table.shape[1],
                     self.seq_lens.data_ptr(), batch, int(max_seq_len), ctypes.c_float(scale),
                     int(partition_size), self.workspace.data_ptr(), self.workspace.numel(), self.stream)
-            if self.grouped:
-                gtail = (*tail[:11], self.prefix_lens.data_ptr(), int(group_size), int(max_prefix_len), *tail[11:-1],
-                         order_ptr, tail[-1])
-                decode_args = (desc, None, 0, 0, None, 0, 0, None, *gtail)
-                fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
-                              vv.stride(1), slot_mapping.data_ptr(), *gtail)
-            else:
-                tail = (*tail[:-1], order_ptr, tail[-1])
-                decode_args = (desc, *tail)
-                fused_args = (desc, kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0),
-                              vv.stride(1), slot_mapping.data_ptr(), *tail)
-            self.calls.append(_LayerCall(fn, append_args, decode_args, fused_args))
+            new_kv = (kk.data_ptr(), kk.stride(0), kk.stride(1), vv.data_ptr(), vv.stride(0), vv.stride(1),
+                      slot_mapping.data_ptr())
+            decode_args, fused_args = {}, {}
+            for shared in (False, True):
+                desc = ctypes.byref(cache.descriptor(shared))
+                if self.grouped:
+                    gtail = (*tail[:11], self.prefix_lens.data_ptr(), int(group_size), int(max_prefix_len),
+                             *tail[11:-1], order_ptr, tail[-1])
+                    decode_args[shared] = (desc, None, 0, 0, None, 0, 0, None, *gtail)
+                    fused_args[shared] = (desc, *new_kv, *gtail)
+                else:
+                    otail = (*tail[:-1], order_ptr, tail[-1])
+                    decode_args[shared] = (desc, *otail)
+                    fused_args[shared] = (desc, *new_kv, *otail)
+            self.calls.append(_LayerCall(fn, append_args, decode_args, fused_args, cache.shared_blocks))
         self._keep = (caches, q, key, value, out)
+        self.scale, self.max_seq_len, self.partition_size = float(scale), int(max_seq_len), int(partition_size)
 
     def prepare(self) -> None:
         """Compute this step's dispatch order from ``seq_lens`` (one launch)."""
@@ -178,30 +190,113 @@ class DecodeStep:
         if rc:
             _lib.check(rc, f"append layer {layer}")
 
-    def attend(self, layer: int) -> None:
+    def attend(self, layer: int, shared_blocks: bool | None = None) -> None:
         self._live.check(layer)
+        c = self.calls[layer]
         fn = self.lib.wkv_paged_decode_gqa_grouped if self.grouped else self.lib.wkv_paged_decode_gqa
-        rc = fn(*self.calls[layer].decode_args)
+        rc = fn(*c.decode_args[c.shared_default if shared_blocks is None else bool(shared_blocks)])
         if rc:
             _lib.check(rc, f"decode layer {layer}")
 
-    def step_layer(self, layer: int) -> None:
+    def step_layer(self, layer: int, shared_blocks: bool | None = None) -> None:
         """Append + attention of one layer in a single launch (plus the partition merge)."""
         self._live.check(layer)
+        c = self.calls[layer]
         fn = self.lib.wkv_paged_decode_gqa_grouped if self.grouped else self.lib.wkv_append_paged_decode_gqa
-        rc = fn(*self.calls[layer].fused_args)
+        rc = fn(*c.fused_args[c.shared_default if shared_blocks is None else bool(shared_blocks)])
         if rc:
             _lib.check(rc, f"append+decode layer {layer}")
 
-    def run(self, fused: bool = True) -> None:
-        """One decode step over every layer (fused append + attention by default)."""
+    def run(self, fused: bool = True, shared_blocks: bool | None = None) -> None:
+        """One decode step over every layer (fused append + attention by default), with
+        the step's read policy ``shared_blocks`` (None = each cache's default)."""
         self.prepare()
         for layer in range(len(self.calls)):
             if fused:
-                self.step_layer(layer)
+                self.step_layer(layer, shared_blocks)
             else:
                 self.append(layer)
-                self.attend(layer)
+                self.attend(layer, shared_blocks)
+
+
+class GraphDecodeStep:
+    """A decode step captured once in a HIP graph and replayed every step.
+
+    The engine runs its decode steps as captured graphs unless told otherwise
+    (``enforce_eager`` defaults to False: wavelet/configs/config.py:1017, passed to
+    the engine at wavelet/inference/engine.py:800). This records the whole step of a
+    ``DecodeStep`` -- the dispatch-order launch and every layer's fused append +
+    attention (+ partition merge) -- into one ``torch.cuda.CUDAGraph``, through the
+    allocation-free entry point (``wkv_append_paged_decode_gqa_noalloc``: split-K
+    partials in the library's static per-GPU scratch, so nothing is allocated and no
+    memset is recorded); ``replay()`` is one graph launch on the current stream.
+
+    The plan's buffers (q, key, value, out, block table, lengths, slots) are the
+    graph's: refill them in place between steps, as for ``DecodeStep``. Its geometry
+    is fixed at capture (batch, ``max_seq_len`` as an upper bound of every length the
+    replays will see, partition, read policy ``shared_blocks``: None = each cache's
+    default). Every call on a GPU shares that GPU's scratch: two plans' replays must
+    not overlap (one stream, or ordered). Geometries whose partials exceed the scratch
+    (``wkv_decode_workspace_size`` > ``WKV_NOALLOC_SCRATCH_BYTES``) are refused. The
+    group-aware decode is not captured here.
+    """
+
+    def __init__(self, step: DecodeStep, *, shared_blocks: bool | None = None) -> None:
+        if step.grouped:
+            raise NotImplementedError("GraphDecodeStep captures the plain decode (no group-aware plan)")
+        self.step = step
+        caches, q, key, value, out = step._keep
+        lib = step.lib
+        batch = step.seq_lens.shape[0]
+        # the launch's partition, waves per workgroup and chunks: partials (and the scratch)
+        # only when a context spans more than one workgroup
+        c0 = caches[0]
+        bt_width = step.block_table.shape[1]
+        part, waves, chunks = decode_plan(batch, c0.num_kv_heads, min(step.max_seq_len, bt_width * c0.block_size),
+                                          c0.block_size, step.partition_size)
+        need = lib.wkv_decode_workspace_size(batch, q[0].shape[1], c0.head_dim,
+                                             min(step.max_seq_len, bt_width * c0.block_size), part * waves)
+        if chunks > 1 and (need < 0 or need > _lib.WKV_NOALLOC_SCRATCH_BYTES):
+            raise ValueError(f"the step's split-K partials need {need} bytes, beyond the "
+                             f"{_lib.WKV_NOALLOC_SCRATCH_BYTES}-byte scratch of the allocation-free decode")
+        dev = caches[0].device
+        self._live = step._live
+        self._live.check_all()
+        order_ptr = step.order.data_ptr() if step.ordered else None
+        bt, sl, slots = step.block_table, step.seq_lens, step.slot_mapping
+
+        def calls(stream: int) -> list[tuple]:
+            out_calls = []
+            for layer, cache in enumerate(caches):
+                qq, kk, vv, oo = q[layer], key[layer], value[layer], out[layer]
+                out_calls.append((ctypes.byref(cache.descriptor(shared_blocks)), kk.data_ptr(), kk.stride(0),
+                                  kk.stride(1), vv.data_ptr(), vv.stride(0), vv.stride(1), slots.data_ptr(),
+                                  qq.data_ptr(), qq.stride(0), qq.stride(1), oo.data_ptr(), qq.shape[1],
+                                  bt.data_ptr(), bt.stride(0), bt.shape[1], sl.data_ptr(), batch,
+                                  step.max_seq_len, ctypes.c_float(step.scale), step.partition_size, order_ptr,
+                                  stream))
+            return out_calls
+
+        fn = lib.wkv_append_paged_decode_gqa_noalloc
+        # the scratch's address is looked up once per device, outside the capture (a
+        # zero-length call validates the arguments and launches nothing)
+        first = calls(torch.cuda.current_stream(dev).cuda_stream)[0]
+        _lib.check(fn(*first[:17], 0, *first[18:]), "allocation-free decode (set-up)")
+        self.graph = torch.cuda.CUDAGraph()
+        capture = torch.cuda.Stream(dev)
+        capture.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.graph(self.graph, stream=capture):
+            cur = torch.cuda.current_stream(dev).cuda_stream
+            if step.ordered:
+                _lib.check(lib.wkv_decode_order(sl.data_ptr(), batch, step.order.data_ptr(), cur), "decode order")
+            for layer, args in enumerate(calls(cur)):
+                _lib.check(fn(*args), f"allocation-free append+decode layer {layer}")
+        torch.cuda.current_stream(dev).wait_stream(capture)
+
+    def replay(self) -> None:
+        """One decode step over every layer: one graph launch."""
+        self._live.check_all()
+        self.graph.replay()
 
 
 class MLADecodeStep:

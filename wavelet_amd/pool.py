@@ -16,6 +16,7 @@ from __future__ import annotations
 
 from typing import Callable
 
+import numpy as np
 import torch
 
 from .blocks import BlockManager
@@ -57,9 +58,11 @@ class KVPool:
             self.layers = [MLALatentCache(num_blocks, block_size, kv_lora_rank, rope_dim, device=device)
                            for _ in range(num_layers)]
         else:
-            # with prefix caching, sequences share blocks: the decode keeps them cached between readers
+            # blocks can be shared (prefix caching, or a fork's prompt whether or not prefix caching is
+            # on), so a decode without a step-level choice keeps K/V cached between readers; a step
+            # whose sequences share nothing streams it instead (decode_shares_blocks)
             self.layers = [PagedKVCache(num_blocks, block_size, num_kv_heads, head_dim, kv_dtype, device=device,
-                                        shared_blocks=enable_prefix_caching)
+                                        shared_blocks=True)
                            for _ in range(num_layers)]
         self.blocks = BlockManager(num_blocks, block_size, enable_prefix_caching=enable_prefix_caching,
                                    max_model_len=max_model_len)
@@ -146,6 +149,34 @@ class KVPool:
     def nbytes(self) -> int:
         """Device bytes of every layer's pool while awake."""
         return sum(c.nbytes for c in self.layers)
+
+    @property
+    def device(self) -> torch.device:
+        return self.layers[0].device
+
+    def copy_blocks(self, pairs) -> None:
+        """Apply copy-on-write pairs ``(src_block, dst_block)`` (``BlockManager.append_slots``)
+        to every layer, GQA or MLA: block ``dst`` becomes a copy of ``src``."""
+        m = np.asarray(pairs, dtype=np.int64).reshape(-1, 2)
+        if m.shape[0] == 0:
+            return
+        dm = torch.from_numpy(m).to(self.device)
+        for c in self.layers:
+            c.copy_blocks(dm)
+
+    def append_slots(self, seq_ids, num_tokens: int = 1) -> torch.Tensor:
+        """Reserve the step's token slots (``BlockManager.append_slots``), apply its
+        copy-on-write pairs to every layer, and return the slot mapping (int64, on the
+        pool's device, sequence-major) for the step's appends."""
+        slots, cow = self.blocks.append_slots(seq_ids, num_tokens)
+        self.copy_blocks(cow)
+        return torch.from_numpy(slots).to(self.device)
+
+    def decode_shares_blocks(self, seq_ids) -> bool:
+        """The read policy of a decode step over ``seq_ids``: True when some block is held by
+        more than one of the pool's sequences (reads then keep K/V cached for the next
+        reader), False when every block is read once (reads stream past the caches)."""
+        return self.blocks.any_shared(seq_ids)
 
     def reset_prefix_cache(self) -> None:
         """Forget cached prompt blocks (after a policy or adapter reload, engine.py:1236-1242)."""
