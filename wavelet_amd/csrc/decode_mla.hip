@@ -616,12 +616,21 @@ __global__ __launch_bounds__(192 * NQ, 1) void decode_mla_kernel(
     float p[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) p[i] = fast_exp2(sv[i] - m_use);
-    l_run = l_run * cr + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
     m_run = m_new;
-    u32x4 pbv;
+    // The packed words stay scalars: hipcc 7.2 hands a bit_cast of an element
+    // of a 4-vector its first element.
+    uint32_t pw[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pbv[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
-    *reinterpret_cast<u32x4 *>(&pt[s & 1][role_w * 1024 + pt_w]) = pbv;
+    for (int i = 0; i < 4; ++i) pw[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+    *reinterpret_cast<u32x4 *>(&pt[s & 1][role_w * 1024 + pt_w]) = u32x4{pw[0], pw[1], pw[2], pw[3]};
+    // The running sum takes the bf16 probabilities the PV products consume, so
+    // numerator and denominator carry the same rounding (a head dominated by a
+    // few tokens then normalises to their exact weights).
+    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[i]), ones, psum, false);
+    l_run = l_run * cr + psum;
     if (grp == 0) corr_s[s & 1][col * NHB + role_w] = cr;
     WKV_PHASE(2)
   };
