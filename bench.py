@@ -55,15 +55,16 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-reps", type=int, default=2, help="passes over all layers for per-launch timing")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU oracle time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--group-aware", action="store_true",
-                    help="qwen2.5-7b-groups: the group-aware decode (each shared prompt block read once per group) "
-                         "instead of decoding every member separately")
+    ap.add_argument("--plain-decode", action="store_true",
+                    help="qwen2.5-7b-groups: decode every member with the plain call (shared prompt blocks and "
+                         "private tokens read with one policy, batch-wide longest-first order) instead of the "
+                         "group-aware decode, the default")
     ap.add_argument("--via-pool", action="store_true",
                     help="qwen3-4b / qwen3-4b-var: build the caches as the engine does -- a KVPool sized by "
                          "KVPool.from_engine_config (gpu_memory_utilization 0.35), tables and slots from its block "
                          "manager, each step's read policy from the manager's reference counts")
     ap.add_argument("--graph", action="store_true",
-                    help="GQA decode workloads (not --group-aware): time replays of the whole step captured in one "
+                    help="GQA decode workloads (not the group-aware qwen2.5-7b-groups default): time replays of the whole step captured in one "
                          "HIP graph (GraphDecodeStep, the allocation-free entry point) instead of eager launches; "
                          "the eager step time is reported beside it")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -393,12 +394,13 @@ def workload(args, torch, dev) -> dict:
     elif name == "qwen2.5-7b-groups":
         w = synth.qwen25_7b_group_workload()
         args.layers = args.layers or 28
-        grouped = bool(getattr(args, "group_aware", False))
+        grouped = not getattr(args, "plain_decode", False)
         kv_dtype = kv_dtype or "fp8_e4m3"
         step, cache_bytes = _gqa_setup(torch, dev, args, w, kv_dtype, grouped=grouped)
         kv_bytes = 1 if kv_dtype == "fp8_e4m3" else 2
         desc = (f"Qwen2.5-7B GRPO groups, {kv_dtype} KV: 28 layers x (append + GQA decode), 32 x 8 seqs, shared "
-                "1024-token prompts" + (" (group-aware: each prompt block read once per group)" if grouped else
+                "1024-token prompts" + (" (group-aware: prompt blocks cached, members' own tokens streamed, "
+                                        "a group's members on one XCD)" if grouped else
                                         " (members decoded separately)"))
     elif name == "deepseek-v3-mla":
         w = synth.deepseek_v3_mla_workload()
@@ -527,8 +529,7 @@ def workload(args, torch, dev) -> dict:
     append = B * 2 * HKV * D * (2 + kv_bytes) + B * 8
     f8 = "true" if kv_bytes == 1 else "false"
     return {"name": name, "step": step, "w": w, "layer_bytes": attn + append, "attn_bytes": attn,
-            "kernel": (f"decode_gqa_grouped_kernel<{D},{f8},true,8> (+ merge_partials_kernel)"
-                       if getattr(step, "grouped", False) else f"decode_gqa_kernel<{D},{f8},true,W>"),
+            "kernel": f"decode_gqa_kernel<{D},{f8},true,W,RP>",
             "dtype": "fp8_e4m3 KV, bf16 q/o" if kv_bytes == 1 else "bf16", "desc": desc, "kv_dtype": kv_dtype,
             "flops_per_layer": 4 * int(L.sum()) * HQ * D, "cache_bytes": cache_bytes,
             "logical_kv_bytes": int(L.sum()) * 2 * HKV * D * kv_bytes,
@@ -699,12 +700,13 @@ def main() -> int:
         print(json.dumps(rec), flush=True)
         return 0
     kernel_name = wl["kernel"]
-    if ",W>" in kernel_name:  # the plain decode: the library's waves per workgroup for this geometry
+    if ",W,RP>" in kernel_name:  # the GQA decode: the library's waves per workgroup for this geometry
         from wavelet_amd import decode_plan
 
         _, waves, _ = decode_plan(w.batch, w.num_kv_heads, int(w.context_lens.max()), w.block_size, args.partition)
-        stream = "true" if wl["stream"] else "false"  # shared prompt blocks keep the default read policy
-        kernel_name = kernel_name.replace(",W>", f",{waves},{stream}>")
+        # read policy: 0 cached (shared blocks), 1 streamed, 2 the group split (prompt cached, own tokens streamed)
+        rp = 2 if getattr(step, "grouped", False) else (1 if wl["stream"] else 0)
+        kernel_name = kernel_name.replace(",W,RP>", f",{waves},{rp}>")
     rec = {
         "metric": "decode-attn+KV-append GB/s (% of HBM peak) & us/step, Qwen3-4B B=64 4k ctx" if headline
         else wl.get("metric", f"decode-attn+KV-append GB/s & us/step, {wl['name']}"),

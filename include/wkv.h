@@ -197,6 +197,19 @@ int wkv_paged_decode_gqa(const wkv_cache_t *cache, const void *q, int64_t q_stri
  * batch order); an addition of this library's. */
 int wkv_decode_order(const int32_t *seq_lens, int32_t batch, int32_t *order, void *stream);
 
+/* The dispatch order for wkv_paged_decode_gqa_grouped over GRPO groups of
+ * group_size consecutive sequences, for the decode geometry the call will get
+ * (num_kv_heads, max_seq_len, block_size, partition_size as passed to it):
+ * longest first, ties by index, within classes of whole groups that the decode
+ * launch maps to the same XCDs, the classes interleaved -- a group's members
+ * then read its prompt through one L2, in the same longest-first rhythm. When
+ * the classes cannot be of equal size (batch not a multiple of group_size
+ * times their number) it is wkv_decode_order's order. One call per step serves
+ * every layer. No reference counterpart; an addition of this library's. */
+int wkv_grouped_decode_order(const int32_t *seq_lens, int32_t batch, int32_t group_size, int32_t num_kv_heads,
+                             int32_t max_seq_len, int32_t block_size, int32_t partition_size, int32_t *order,
+                             void *stream);
+
 /* The launch shape the two GQA decode calls use for this geometry (host
  * only, no GPU): the partition size (partition_size, or the library's choice
  * when 0), the waves per workgroup and the workgroups (chunks) per sequence
@@ -276,21 +289,20 @@ int wkv_append_paged_decode_gqa_noalloc(const wkv_cache_t *cache, const void *ke
  * group may be short), and the first prefix_lens[g] tokens of every member are
  * stored in the same physical blocks -- identical block-table entries, as
  * SamplingParams(n=num_generations) leaves them (engine.py:69-90) and
- * BlockManager.share_prefix builds them. The shared prompt blocks are read
- * once per (group, KV head) for all the group's query rows instead of once per
- * member (a plain decode re-reads them group_size times); each member's own
- * tokens are attended as in wkv_paged_decode_gqa, and the parts are merged by
- * log-sum-exp. The result equals wkv_paged_decode_gqa (or, with key, value and
- * slot_mapping given, wkv_append_paged_decode_gqa) on the same inputs, to
- * floating-point reassociation. key, value and slot_mapping are all NULL for
- * attention only. The kernel cuts each group's prefix to whole blocks held by
- * every member (and before a token this call appends); max_prefix_len bounds
- * prefix_lens. workspace: wkv_grouped_decode_workspace_size() bytes.
- * seq_order (optional, as for wkv_paged_decode_gqa) dispatches the members'
- * own tokens longest first; the result does not depend on it (an entry
- * outside 0..batch-1 leaves that sequence's output unspecified). No
- * reference counterpart computes this (vLLM decodes each member separately);
- * the group semantics are the reference's (engine.py:69-90, :1034-1038). */
+ * BlockManager.share_prefix builds them. The attention is wkv_paged_decode_gqa's
+ * (or, with key, value and slot_mapping given, wkv_append_paged_decode_gqa's),
+ * bit for bit; what the groups change is how the cache is read: the group's
+ * prompt blocks keep the default cache policy, so its members' reads of one
+ * block meet in the L2 and the last-level cache, while each member's own tokens
+ * are streamed past them (non-temporal loads). With seq_order from
+ * wkv_grouped_decode_order, the members' workgroups of one KV head also run
+ * on one XCD (one L2). key, value and slot_mapping are all NULL for attention
+ * only. prefix_lens values above max_prefix_len are read as max_prefix_len;
+ * prefix_lens only steers the read policy (any values give the same result).
+ * workspace: wkv_grouped_decode_workspace_size() bytes (the plain decode's).
+ * seq_order as for wkv_paged_decode_gqa. No reference counterpart computes
+ * this (vLLM decodes each member separately); the group semantics are the
+ * reference's (engine.py:69-90, :1034-1038). */
 int64_t wkv_grouped_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim,
                                           int32_t max_seq_len, int32_t max_prefix_len, int32_t partition_size);
 

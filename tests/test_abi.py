@@ -115,6 +115,15 @@ def test_decode_rejects_bad_arguments_before_launch():
     assert o(None, 4, 16, None) == _lib.WKV_ERR_INVALID
     assert o(16, 4, None, None) == _lib.WKV_ERR_INVALID
     assert o(None, 0, None, None) == _lib.WKV_OK
+    # the group-aware order: the same checks plus the group and the decode geometry
+    go = lib.wkv_grouped_decode_order
+    assert go(16, 8, 0, 4, 4096, 16, 0, 16, None) == _lib.WKV_ERR_INVALID  # group_size 0
+    assert go(16, 8, 9, 4, 4096, 16, 0, 16, None) == _lib.WKV_ERR_INVALID  # group larger than the batch
+    assert go(16, 8, 4, 0, 4096, 16, 0, 16, None) == _lib.WKV_ERR_INVALID  # no KV heads
+    assert go(16, 8, 4, 4, 4096, 24, 0, 16, None) == _lib.WKV_ERR_INVALID  # block size not a multiple of 16
+    assert go(None, 8, 4, 4, 4096, 16, 0, 16, None) == _lib.WKV_ERR_INVALID
+    assert go(16, 8, 4, 4, 4096, 16, 0, None, None) == _lib.WKV_ERR_INVALID
+    assert go(None, 0, 0, 0, 0, 0, 0, None, None) == _lib.WKV_OK  # empty batch: a no-op
 
 
 @host_only

@@ -231,8 +231,8 @@ def test_plan_qwen25_05b_b128(cuda):
 
 @pytest.mark.parametrize("grouped", [False, True])
 def test_plan_qwen25_7b_fp8_groups_256_sequences(cuda, grouped):
-    """All 32 groups x 8 members; the plain plan is the bench default, the group-aware one
-    is --group-aware."""
+    """All 32 groups x 8 members; the group-aware plan is the bench default, the plain one
+    is --plain-decode."""
     w = synth.qwen25_7b_group_workload()
     _run_gqa_plan(cuda, "qwen2.5-7b-groups" + ("-grouped" if grouped else ""), w, "fp8_e4m3", grouped=grouped)
 

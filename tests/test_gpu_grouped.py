@@ -4,10 +4,12 @@ Groups are built the way the engine builds them: one prompt allocated through
 ``BlockManager`` and forked to every member (shared physical blocks), private
 generated tokens per member, then a decode step whose append copies a still
 shared partially filled block first (copy-on-write). ``prefix_lens`` comes from
-``BlockManager.shared_prefix_tokens``. The grouped call must equal the plain
-call on the same inputs (bf16: to the attention tolerance, the summation order
-differs; the fused append leaves the cache bit-identical) and the oracle.
-Unowned bf16 slots hold NaN, so a read outside any context would surface.
+``BlockManager.shared_prefix_tokens``. The grouped call reads the prompt with
+another cache policy than the members' own tokens but over the same tiles, so
+it must equal the plain call on the same inputs bit for bit (attention only,
+and fused with the step's append: outputs and cache), in any dispatch order
+(batch order, ``grouped_decode_order``), and match the oracle. Unowned bf16
+slots hold NaN, so a read outside any context would surface.
 """
 
 import math
@@ -18,7 +20,8 @@ import torch
 
 from kvcase import bits_of, check_attention, to_dev_bits
 from oracle import fp8, paged
-from wavelet_amd import BlockManager, PagedKVCache, paged_decode_gqa, paged_decode_gqa_grouped, synth
+from wavelet_amd import (BlockManager, PagedKVCache, decode_plan, grouped_decode_order, paged_decode_gqa,
+                         paged_decode_gqa_grouped, synth)
 
 pytestmark = pytest.mark.gpu
 
@@ -110,7 +113,7 @@ def test_grouped_decode_matches_plain_and_oracle(cuda, kv_dtype, hq, hkv, d, bs,
     kc, vc, ks, vs = _fill(m, ids, bs, NB, hkv, d, prompts, tag, is_fp8, skip_last=1)
     pre = np.array([m.shared_prefix_tokens([(g, j) for j in range(gs)]) for g in range(n_groups)], np.int32)
     assert pre.max() > 0
-    caches = [PagedKVCache(NB, bs, hkv, d, kv_dtype=kv_dtype, device=cuda) for _ in range(2)]
+    caches = [PagedKVCache(NB, bs, hkv, d, kv_dtype=kv_dtype, device=cuda) for _ in range(3)]
     for c in caches:
         _upload(c, kc, vc, ks, vs, cuda)
     scale = 1 / math.sqrt(d)
@@ -127,22 +130,29 @@ def test_grouped_decode_matches_plain_and_oracle(cuda, kv_dtype, hq, hkv, d, bs,
         lens0 = dlens - 1
         plain = paged_decode_gqa(q, caches[0], dbt, lens0, scale, partition_size=p)
         grouped = paged_decode_gqa_grouped(q, caches[0], dbt, lens0, dpre, gs, scale, partition_size=p)
-        torch.testing.assert_close(grouped.float(), plain.float(), atol=2e-2, rtol=1e-2,
-                                   msg=lambda s: f"grouped vs plain, attention only (P={p}): {s}")
-        # the whole step, fused: the grouped call appends into caches[1]
+        assert torch.equal(grouped.view(torch.int16), plain.view(torch.int16)), f"grouped vs plain (P={p})"
+        order = grouped_decode_order(lens0, gs, hkv, int(lens0.max()), bs, p)
+        ordered = paged_decode_gqa_grouped(q, caches[0], dbt, lens0, dpre, gs, scale, partition_size=p,
+                                           seq_order=order)
+        assert torch.equal(ordered.view(torch.int16), plain.view(torch.int16)), f"grouped, ordered (P={p})"
+        # the whole step, fused: the grouped call appends into caches[1], the plain one into caches[2]
         if p == 0:
             caches[0].append(kn, vn, dslots)
             ref_out = paged_decode_gqa(q, caches[0], dbt, dlens, scale)
             out = paged_decode_gqa_grouped(q, caches[1], dbt, dlens, dpre, gs, scale, new_key=kn, new_value=vn,
                                            slot_mapping=dslots)
+            plain_fused = paged_decode_gqa(q, caches[2], dbt, dlens, scale, new_key=kn, new_value=vn,
+                                           slot_mapping=dslots)
             torch.cuda.synchronize()
-            assert torch.equal(caches[0].k.view(torch.uint8), caches[1].k.view(torch.uint8)), "K differs"
-            assert torch.equal(caches[0].v.view(torch.uint8), caches[1].v.view(torch.uint8)), "V differs"
-            if is_fp8:
-                assert torch.equal(caches[0].k_scale, caches[1].k_scale)
-                assert torch.equal(caches[0].v_scale, caches[1].v_scale)
+            for c in (caches[1], caches[2]):
+                assert torch.equal(caches[0].k.view(torch.uint8), c.k.view(torch.uint8)), "K differs"
+                assert torch.equal(caches[0].v.view(torch.uint8), c.v.view(torch.uint8)), "V differs"
+                if is_fp8:
+                    assert torch.equal(caches[0].k_scale, c.k_scale)
+                    assert torch.equal(caches[0].v_scale, c.v_scale)
+            assert torch.equal(out.view(torch.int16), plain_fused.view(torch.int16)), "grouped fused vs plain fused"
             torch.testing.assert_close(out.float(), ref_out.float(), atol=2e-2, rtol=1e-2,
-                                       msg=lambda s: f"grouped fused vs plain: {s}")
+                                       msg=lambda s: f"grouped fused vs append + plain: {s}")
     # oracle on the final cache (after the append)
     if is_fp8:
         paged.append_fp8(kc, vc, ks, vs, kn_bits, vn_bits, new_slots)
@@ -156,7 +166,7 @@ def test_grouped_decode_matches_plain_and_oracle(cuda, kv_dtype, hq, hkv, d, bs,
 
 def test_grouped_decode_prefix_claims(cuda):
     """prefix_lens of 0 (no sharing used), below the shared blocks, unaligned, and above the
-    shortest member all give the plain result (the kernel cuts to whole blocks every member holds)."""
+    shortest member all give the plain result bit for bit (they steer the read policy only)."""
     hq, hkv, d, bs, gs = 28, 4, 128, 16, 8
     tag = "grpclaims"
     NB = 1024
@@ -176,8 +186,7 @@ def test_grouped_decode_prefix_claims(cuda):
     for claim in ([0, 0], [100, 37], [shared[0], shared[1]], [shared[0] - 5, 1]):
         pre = torch.tensor(claim, dtype=torch.int32, device=cuda)
         got = paged_decode_gqa_grouped(q, cache, dbt, dlens, pre, gs, scale)
-        torch.testing.assert_close(got.float(), plain.float(), atol=2e-2, rtol=1e-2,
-                                   msg=lambda s: f"claim {claim}: {s}")
+        assert torch.equal(got.view(torch.int16), plain.view(torch.int16)), f"claim {claim}"
     ref = _oracle(q_bits, kc, vc, None, None, bt, lens, scale, NB, bs, hkv, d)
     check_attention(paged.bf16_to_f32(bits_of(got)), ref, "grouped claims")
 
@@ -218,7 +227,40 @@ def test_grouped_decode_ragged_last_group_and_empty(cuda):
     scale = 1 / math.sqrt(d)
     got = paged_decode_gqa_grouped(q, cache, dbt, dlens, pre, gs, scale, partition_size=32)
     plain = paged_decode_gqa(q, cache, dbt, dlens, scale, partition_size=32)
-    torch.testing.assert_close(got.float(), plain.float(), atol=2e-2, rtol=1e-2)
+    assert torch.equal(got.view(torch.int16), plain.view(torch.int16))
     assert torch.count_nonzero(got[3]) == 0  # empty context: zeros
     ref = _oracle(q_bits, kc, vc, None, None, bt, lens, scale, NB, bs, hkv, d)
     check_attention(paged.bf16_to_f32(bits_of(got)), ref, "grouped ragged")
+
+
+def _expected_grouped_order(lens, gs, hkv, max_seq, bs, partition):
+    """The order's definition: classes of whole groups (group g in class g % n), n the
+    number of XCD classes of the launch (8 / gcd(8, chunks * Hkv), 1 when the classes
+    would be unequal); stable longest-first within a class; rank r of class c at r*n + c."""
+    _, _, chunks = decode_plan(len(lens), hkv, max_seq, bs, partition)
+    n = 8 // math.gcd(8, chunks * hkv)
+    if len(lens) % (gs * n):
+        n = 1
+    out = np.empty(len(lens), np.int64)
+    for c in range(n):
+        idx = np.array([i for i in range(len(lens)) if (i // gs) % n == c])
+        ranked = idx[np.argsort(-lens[idx].astype(np.int64), kind="stable")]
+        out[np.arange(len(ranked)) * n + c] = ranked
+    return out, n
+
+
+@pytest.mark.parametrize("batch,gs,hkv,max_seq,part,n_cls", [
+    (256, 8, 4, 4096, 0, 2),   # Qwen2.5-7B groups: one workgroup per (sequence, KV head)
+    (48, 3, 1, 1000, 0, 8),    # one KV head: eight classes
+    (64, 4, 2, 2000, 128, 2),  # two chunks per sequence
+    (44, 3, 1, 1000, 0, 1),    # eight classes would be unequal: the plain longest-first order
+    (40, 5, 8, 4096, 0, 1),    # eight KV heads: a head already stays on one XCD
+])
+def test_grouped_decode_order(cuda, batch, gs, hkv, max_seq, part, n_cls):
+    rng = np.random.default_rng(batch + gs)
+    lens = rng.integers(0, max_seq + 1, batch).astype(np.int32)
+    lens[: batch // 4] = lens[0]  # ties
+    want, n = _expected_grouped_order(lens, gs, hkv, max_seq, 16, part)
+    assert n == n_cls
+    got = grouped_decode_order(torch.from_numpy(lens).to(cuda), gs, hkv, max_seq, 16, part).cpu().numpy()
+    np.testing.assert_array_equal(got, want)

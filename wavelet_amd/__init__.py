@@ -8,7 +8,8 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
   ``decode_order`` -- a step's longest-first dispatch order for the former,
   ``decode_plan`` -- its launch shape;
 * ``paged_decode_gqa_grouped`` -- the same for GRPO groups, reading each
-  group's shared prompt blocks once;
+  group's shared prompt blocks through the caches and the members' own tokens
+  streamed; ``grouped_decode_order`` -- its dispatch order;
 * ``prefill_gqa`` -- varlen (chunked) prefill that appends the prompt's K/V
   and attends causally over the paged context;
 * ``BlockManager`` -- host-side block allocation with ref-counted prefix
@@ -19,7 +20,8 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
   top_p, repetition penalty; processed logprobs and the sampling mask).
 """
 
-from .attention import decode_order, decode_plan, paged_decode_gqa, paged_decode_gqa_grouped, paged_decode_mla, prefill_gqa
+from .attention import (decode_order, decode_plan, grouped_decode_order, paged_decode_gqa, paged_decode_gqa_grouped,
+                        paged_decode_mla, prefill_gqa)
 from .blocks import BlockManager
 from .cache import MLALatentCache, PagedKVCache, validate_group_prefix, validate_tables
 from .pool import KVPool
@@ -31,6 +33,7 @@ __all__ = [
     "MLALatentCache",
     "PagedKVCache",
     "decode_order",
+    "grouped_decode_order",
     "decode_plan",
     "paged_decode_gqa",
     "paged_decode_gqa_grouped",

@@ -61,6 +61,8 @@ _SIGNATURES = {
     "wkv_mla_copy_blocks": (c_int, [POINTER(WkvMlaCache), c_void_p, c_int64, c_void_p]),
     "wkv_decode_workspace_size": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "wkv_decode_order": (c_int, [c_void_p, c_int32, c_void_p, c_void_p]),
+    "wkv_grouped_decode_order": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
+                                         c_void_p]),
     "wkv_decode_plan": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "wkv_paged_decode_gqa": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_void_p]),
     "wkv_append_paged_decode_gqa": (c_int, [POINTER(WkvCache), c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_void_p]),

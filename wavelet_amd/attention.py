@@ -93,6 +93,28 @@ def decode_order(seq_lens: torch.Tensor, out: torch.Tensor | None = None) -> tor
     return out
 
 
+def grouped_decode_order(seq_lens: torch.Tensor, group_size: int, num_kv_heads: int, max_seq_len: int,
+                         block_size: int, partition_size: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Dispatch order for ``paged_decode_gqa_grouped`` (GRPO groups of ``group_size``
+    consecutive sequences): longest first within classes of whole groups that the
+    decode launch maps to the same XCDs, the classes interleaved, so that a group's
+    members read its prompt through one L2 (``decode_order`` when the classes cannot
+    be of equal size). The geometry is the one the grouped decode calls will get."""
+    if seq_lens.dtype != torch.int32 or seq_lens.dim() != 1 or not seq_lens.is_contiguous():
+        raise ValueError("seq_lens must be a contiguous int32 vector")
+    batch = seq_lens.shape[0]
+    if out is None:
+        out = torch.empty(batch, dtype=torch.int32, device=seq_lens.device)
+    elif (out.dtype != torch.int32 or tuple(out.shape) != (batch,) or not out.is_contiguous()
+          or out.device != seq_lens.device):
+        raise ValueError(f"out must be a contiguous int32 [{batch}] tensor on {seq_lens.device}")
+    _lib.check(_lib.load().wkv_grouped_decode_order(seq_lens.data_ptr(), batch, int(group_size), int(num_kv_heads),
+                                                     int(max_seq_len), int(block_size), int(partition_size),
+                                                     out.data_ptr(), _stream(seq_lens.device)),
+               "grouped_decode_order")
+    return out
+
+
 def paged_decode_gqa(
     q: torch.Tensor,
     cache: PagedKVCache,
@@ -195,18 +217,19 @@ def paged_decode_gqa_grouped(
     slot_mapping: torch.Tensor | None = None,
     seq_order: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """``paged_decode_gqa`` for GRPO groups that read their shared prompt once.
+    """``paged_decode_gqa`` for GRPO groups, reading their shared prompt through the caches.
 
     Sequences ``g*group_size .. g*group_size+group_size-1`` form group ``g``;
     ``prefix_lens [n_groups]`` int32 gives the leading tokens whose physical
     blocks every member's table shares (``BlockManager.shared_prefix_tokens``).
-    The result equals ``paged_decode_gqa`` on the same inputs (to fp32
-    reassociation); the shared blocks are streamed once per group and KV head
-    for all of the group's query rows. Optional fused append as in
-    ``paged_decode_gqa`` (the group semantics follow ``SamplingParams(n=...)``,
-    wavelet/inference/engine.py:69-90). ``seq_order`` (``decode_order``)
-    dispatches the members' own tokens longest first; the result is the same
-    bit for bit.
+    The result is ``paged_decode_gqa``'s on the same inputs, bit for bit (with
+    the fused append: ``paged_decode_gqa`` after ``append``); the groups steer
+    how the cache is read: the prompt blocks keep the default cache policy, so
+    the members' reads of one block meet in the L2 and the last-level cache,
+    and each member's own tokens are streamed past them. ``seq_order`` from
+    ``grouped_decode_order`` also runs a group's members on one XCD. Optional
+    fused append as in ``paged_decode_gqa`` (the group semantics follow
+    ``SamplingParams(n=...)``, wavelet/inference/engine.py:69-90).
     """
     if not isinstance(cache, PagedKVCache):
         raise ValueError("cache must be a PagedKVCache")

@@ -382,13 +382,15 @@ def validate_group_prefix(block_table, seq_lens, prefix_lens, group_size: int, b
                           appending: bool = False) -> None:
     """Debug check (synchronises) of a group-aware decode's ``prefix_lens`` claim.
 
-    ``paged_decode_gqa_grouped`` reads group ``g``'s first ``n_g`` blocks once,
-    through the first member's block table, for every member, where ``n_g =
-    min(prefix_lens[g], shortest member context (minus the token a fused
-    append adds)) // block_size``. It trusts the claim; a member whose table
-    differs inside those blocks would silently attend the first member's
-    blocks. This raises ValueError naming the first such (group, member,
-    block). Accepts torch tensors (any device) or numpy arrays.
+    The claim: group ``g``'s first ``n_g`` blocks are the same physical blocks in
+    every member's table, ``n_g = min(prefix_lens[g], shortest member context
+    (minus the token a fused append adds)) // block_size``.
+    ``paged_decode_gqa_grouped`` reads every member through its own table, so a
+    wrong claim cannot change its result; it reads the claimed tokens with the
+    cached policy, so a claim that covers private blocks only wastes cache
+    capacity on them. This raises ValueError naming the first (group, member,
+    block) that breaks the claim. Accepts torch tensors (any device) or numpy
+    arrays.
     """
     import numpy as np
 

@@ -44,16 +44,26 @@ __device__ __forceinline__ float sink_weight(const float *sinks, int hq, float m
 // owns partition c*W + w of P_tok tokens. The waves of a workgroup merge
 // their partials through LDS; a context longer than one chunk leaves one
 // partial per chunk for merge_partials_kernel.
-// STREAM: K/V tiles are read with the non-temporal policy (blocks read once);
-// a compile-time choice, as a runtime one costs the tile pipeline its schedule.
-template <int D, bool FP8, bool APPEND, int W, bool STREAM>
+// RP, the read policy of the K/V tiles -- a compile-time choice, as a per-tile
+// one costs the tile pipeline its schedule:
+//   kReadCached:   the default policy (blocks that several sequences read);
+//   kReadStreamed: non-temporal loads (blocks read once);
+//   kReadSplit:    GRPO groups of group_size consecutive sequences: the first
+//     prefix_lens[b / group_size] tokens of sequence b -- the group's prompt,
+//     whose blocks every member reads -- keep the default policy, so the
+//     members' reads of one prompt block meet in the caches, and the member's
+//     own tokens are streamed. The cut is a multiple of 16 tokens from the
+//     partition start, so the tiles, and the result, are the plain call's.
+constexpr int kReadCached = 0, kReadStreamed = 1, kReadSplit = 2;
+
+template <int D, bool FP8, bool APPEND, int W, int RP>
 __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ ks, float *__restrict__ vs,
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ out,
     float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
     int Mb, int max_seq, const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ order, int Hq, int Hkv,
     int G, int BS, int64_t NB, float scale_log2, int P_tok, int max_chunks, StepAppend ap,
-    const float *__restrict__ sinks) {
+    const float *__restrict__ sinks, const int32_t *__restrict__ prefix_lens, int group_size, int max_prefix) {
   const int chunk = blockIdx.x, kvh = blockIdx.y;
   // The wave index is uniform across the wave; saying so keeps everything
   // derived from it (partition, block ids, buffer resources) in scalar registers.
@@ -86,6 +96,12 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     load_q<D, FP8>(qop, q + b * q_sb + static_cast<int64_t>(kvh * G + (col < G ? col : 0)) * q_sh, col < G, grp);
   }
 
+  // The group's shared prompt: tokens [0, cut), read with the default policy.
+  int cut = 0;
+  if constexpr (RP == kReadSplit) {
+    cut = prefix_lens[b / group_size];
+    cut = cut < max_prefix ? cut : max_prefix;
+  }
   L = L < max_seq ? L : max_seq;  // max_seq <= block-table width * BS: every read stays in the table
   if (L <= 0) {
     if (chunk == 0 && wave == 0 && col < G) {  // empty context: zeros
@@ -149,8 +165,26 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
   if (active) {
     const int t_end = (t_begin + P_seq) < L ? (t_begin + P_seq) : L;
     const bool from_regs = APPEND && !FP8 && owns_new;  // last token comes from the inputs
-    attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, from_regs ? L - 1 : t_end, kvh, Hkv, BS,
-                             NB, scale_log2, lane, col, grp, STREAM);
+    const int te = from_regs ? L - 1 : t_end;
+    if constexpr (RP == kReadSplit) {
+      // [t_begin, c) of the shared prompt cached, [c, te) streamed; c - t_begin is
+      // a multiple of 16, so both ranges hold the partition's own 16-token tiles.
+      int c = cut - t_begin;
+      c = t_begin + (c > 0 ? (c & ~15) : 0);
+      if (c > t_begin)
+        attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, te < c ? te : c, kvh, Hkv, BS, NB,
+                                 scale_log2, lane, col, grp, false);
+      if (te > c) {
+        // the streamed range's block ids, lane i = its i-th block
+        const int sh = c / BS - blk_first;
+        const int mb = sh > 0 ? __shfl(my_blk, (lane + sh) & 63, 64) : my_blk;
+        attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, mb, c, te, kvh, Hkv, BS, NB, scale_log2, lane, col, grp,
+                                 true);
+      }
+    } else {
+      attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, te, kvh, Hkv, BS, NB, scale_log2, lane,
+                               col, grp, RP == kReadStreamed);
+    }
     if constexpr (APPEND && !FP8) {
       if (owns_new) {
         Tile<D, FP8> tn;
@@ -329,269 +363,6 @@ struct PlainSlots {
   }
 };
 
-// ---------------------------------------------------------------------------
-// Group-aware decode (GRPO groups): sequences g*gs .. g*gs+gs-1 form group g
-// and store the group's first prefix tokens in the same physical blocks. One
-// launch runs two kinds of workgroups:
-//   prefix role: per (group, KV head, prefix partition), the shared blocks are
-//     streamed once for all gs*G query rows of the group -- the MFMA columns
-//     are (member, head) pairs instead of one sequence's heads, and the W waves
-//     of the workgroup take different 16-row tiles of the same tokens, so each
-//     tile is fetched from HBM once and served to the others from cache;
-//   suffix role: per (sequence, KV head, chunk), the ordinary decode over the
-//     sequence's private tokens (with the step's fused append).
-// Both leave (m, l, o) partials; merge_partials_kernel combines them.
-struct GroupGeom {
-  const int32_t *prefix_lens;  // [n_groups] leading tokens the caller declares shared
-  int gs;                      // sequences per group (the last group may be short)
-  int nrt;                     // 16-row tiles of a group's gs * G query rows
-  int rows_w;                  // row tiles per prefix workgroup: min(nrt, W)
-  int nrtb;                    // prefix workgroups across the row tiles: ceil(nrt / rows_w)
-  int ppw;                     // prefix partitions per workgroup: W / rows_w when nrt <= W, else 1
-  int npb;                     // prefix workgroups across the partitions: ceil(npp / ppw)
-  int p_pre;                   // most tokens per prefix partition (a block multiple)
-  int npp;                     // prefix partitions: partial slots 0 .. npp-1
-  int nsc;                     // suffix chunks: partial slots npp .. npp+nsc-1
-  int n_pre_wgs;               // workgroups of the prefix role; they come first (their
-                               // waves are among the longest), then the suffix role's
-  int append;                  // 1 when the suffix role appends the step's token
-};
-
-// Tokens of group g that the prefix role attends: the declared prefix, cut to
-// what every member holds (excluding a token this step appends, whose block an
-// fp8 append may rewrite), to the launch's npp partitions, and down to whole
-// blocks (so suffix partitions stay block-aligned for the fused append).
-// (The members' lengths are read lane-parallel and reduced across the wave: one
-// memory round trip, not one per member.) Call with the whole wave active.
-__device__ __forceinline__ int group_prefix(const GroupGeom &gg, const int32_t *__restrict__ seq_lens, int g,
-                                            int batch, int max_seq, int BS) {
-  const int lane = threadIdx.x & 63;
-  const int b0 = g * gg.gs;
-  const int b1 = (b0 + gg.gs) < batch ? (b0 + gg.gs) : batch;
-  int pre = gg.prefix_lens[g];
-  for (int b = b0 + lane; b < b1; b += 64) {
-    int L = seq_lens[b];
-    L = L < max_seq ? L : max_seq;
-    L -= gg.append;
-    pre = pre < L ? pre : L;
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const int other = __shfl_xor(pre, o, 64);
-    pre = pre < other ? pre : other;
-  }
-  const int cap = gg.npp * gg.p_pre;
-  pre = pre < cap ? pre : cap;
-  pre = pre > 0 ? pre : 0;
-  return __builtin_amdgcn_readfirstlane(pre / BS * BS);
-}
-
-// Tokens per prefix partition of a group whose prefix is pre > 0 tokens: the
-// ceil(pre / p_pre) partitions balanced, in whole blocks (<= p_pre).
-__device__ __forceinline__ int prefix_partition(int pre, int p_pre, int BS) {
-  const int n = (pre + p_pre - 1) / p_pre;
-  int p = (pre + n - 1) / n;
-  p = (p + BS - 1) / BS * BS;
-  return __builtin_amdgcn_readfirstlane(p);
-}
-
-template <int D, bool FP8, bool APPEND, int W>
-__global__ __launch_bounds__(64 * W) void decode_gqa_grouped_kernel(
-    uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ ks, float *__restrict__ vs,
-    const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, float *__restrict__ part_o,
-    float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride, int Mb, int max_seq,
-    const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ order, int batch, int Hq, int Hkv, int G,
-    int BS, int64_t NB, float scale_log2, int P_tok, StepAppend ap, GroupGeom gg) {
-  constexpr int stream = 1;  // the suffix role's tokens are private to their sequence: read once
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-  const int slots = gg.npp + gg.nsc;
-  DecodeState<D, FP8> st;
-#pragma unroll
-  for (int n = 0; n < D / 16; ++n) st.o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
-  st.l = 0.f;
-
-  if (static_cast<int>(blockIdx.x) < gg.n_pre_wgs) {
-    // ---- prefix role: workgroup (group, KV head, row-tile block, partition
-    // block); wave = (partition of the block, row tile of the block)
-    int r = static_cast<int>(blockIdx.x);
-    const int pb = r % gg.npb;
-    r /= gg.npb;
-    const int kvh = r % Hkv;
-    r /= Hkv;
-    const int rt = (r % gg.nrtb) * gg.rows_w + wave % gg.rows_w;
-    const int p = pb * gg.ppw + wave / gg.rows_w;
-    const int g = __builtin_amdgcn_readfirstlane(r / gg.nrtb);
-    if (wave / gg.rows_w >= gg.ppw || rt >= gg.nrt || p >= gg.npp) return;  // waves leave independently here
-    const int pre = group_prefix(gg, seq_lens, g, batch, max_seq, BS);
-    if (pre <= 0) return;
-    const int ppart = prefix_partition(pre, gg.p_pre, BS);
-    const int t_begin = p * ppart;
-    if (t_begin >= pre) return;
-    const int t_end = (t_begin + ppart) < pre ? (t_begin + ppart) : pre;
-    const int b0 = g * gg.gs;
-    // This lane's column is query row rt*16 + col of the group: (member, head).
-    const int row = rt * 16 + col;
-    const int member = row / G, h = row - member * G;
-    const int b = b0 + member;
-    const bool valid = member < gg.gs && b < batch;
-    const int blk_first = t_begin / BS;
-    int my_blk = -1;
-    if (blk_first + lane < Mb) my_blk = bt[b0 * bt_stride + blk_first + lane];
-    bf16x8 qop[D / 32];
-    load_q<D, FP8>(qop, q + (valid ? b : b0) * q_sb + static_cast<int64_t>(kvh * G + (valid ? h : 0)) * q_sh,
-                   valid, grp);
-    // the shared prompt blocks: the workgroup's four row-tile waves read each
-    // tile, so the loads keep the default cache policy
-    attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, t_end, kvh, Hkv, BS, NB, scale_log2, lane,
-                             col, grp, false);
-    float l = st.l + __shfl_xor(st.l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    if (!valid) return;
-    const int64_t prow = (static_cast<int64_t>(b) * Hq + kvh * G + h) * slots + p;
-    float *po = part_o + prow * D;
-#pragma unroll
-    for (int n = 0; n < D / 16; ++n) *reinterpret_cast<floatx4 *>(po + 16 * n + 4 * grp) = st.o[n];
-    if (grp == 0) {
-      part_ml[2 * prow] = st.m;
-      part_ml[2 * prow + 1] = l;
-    }
-    return;
-  }
-
-  // ---- suffix role: workgroup (sequence or dispatch rank, KV head, chunk of W partitions)
-  int r = static_cast<int>(blockIdx.x) - gg.n_pre_wgs;
-  const int chunk = r % gg.nsc;
-  r /= gg.nsc;
-  const int kvh = r % Hkv;
-  int b = __builtin_amdgcn_readfirstlane(r / Hkv);
-  if (order != nullptr) {  // longest contexts first: the short ones fill in behind them
-    b = __builtin_amdgcn_readfirstlane(order[b]);
-    if (b < 0 || b >= batch) return;  // not an entry of a permutation of the batch
-  }
-  const int pre = group_prefix(gg, seq_lens, b / gg.gs, batch, max_seq, BS);
-  int L = seq_lens[b];
-  L = L < max_seq ? L : max_seq;
-  const int S = L - pre;  // this sequence's own tokens
-  const int nchunks = S > 0 ? (S + W * P_tok - 1) / (W * P_tok) : 0;
-  if (chunk >= nchunks) return;  // the whole workgroup leaves together
-  const int P_seq = balanced_partition(S, W, P_tok, BS);
-  const int part = chunk * W + wave;
-  const int t_begin = pre + part * P_seq;
-  const int blk_first = t_begin / BS;
-  int my_blk = -1;
-  if (blk_first + lane < Mb) my_blk = bt[b * bt_stride + blk_first + lane];
-  bf16x8 qop[D / 32];
-  load_q<D, FP8>(qop, q + b * q_sb + static_cast<int64_t>(kvh * G + (col < G ? col : 0)) * q_sh, col < G, grp);
-  const int nparts = (S + P_seq - 1) / P_seq;
-  const bool active = part < nparts;
-  const bool owns_new = APPEND && part == nparts - 1;
-
-  // Fused append, as in decode_gqa_kernel: the new token's block lies wholly in
-  // the last suffix partition (pre and P_tok are block multiples).
-  uint32_t nk = 0, nv = 0;
-  int64_t slot = -1;
-  if constexpr (APPEND) {
-    if (owns_new) {
-      slot = ap.slots[b];
-      if constexpr (FP8) {
-        if (slot >= 0 && slot / BS < NB) {
-          const int64_t blk = slot / BS;
-          const int off = static_cast<int>(slot % BS);
-          fp8_append_one<D, false>(kc, ks, ap.key, ap.kst, ap.ksh, ap.slots, b, 1, blk, off, kvh, Hkv, BS);
-          fp8_append_one<D, true>(vc, vs, ap.val, ap.vst, ap.vsh, ap.slots, b, 1, blk, off, kvh, Hkv, BS);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      } else {
-        if (lane < D / 2) {
-          nk = reinterpret_cast<const uint32_t *>(ap.key + b * ap.kst + kvh * ap.ksh)[lane];
-          nv = reinterpret_cast<const uint32_t *>(ap.val + b * ap.vst + kvh * ap.vsh)[lane];
-        }
-      }
-    }
-  }
-  if (active) {
-    const int t_end = (t_begin + P_seq) < L ? (t_begin + P_seq) : L;
-    const bool from_regs = APPEND && !FP8 && owns_new;
-    attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, from_regs ? L - 1 : t_end, kvh, Hkv, BS,
-                             NB, scale_log2, lane, col, grp, stream != 0);
-    if constexpr (APPEND && !FP8) {
-      if (owns_new) {
-        Tile<D, FP8> tn;
-        new_token_tile<D>(tn, nk, nv, col, grp);
-        attend_tile<D, FP8>(st, tn, qop, scale_log2, grp);
-        if (slot >= 0 && slot / BS < NB && lane < D / 2) {
-          const int64_t nblk_id = slot / BS;
-          const int off = static_cast<int>(slot % BS);
-          uint16_t *kd = reinterpret_cast<uint16_t *>(kc) +
-                         (((nblk_id * Hkv + kvh) * (D / 8) + (lane >> 2)) * BS + off) * 8 + (lane & 3) * 2;
-          *reinterpret_cast<uint32_t *>(kd) = nk;
-          uint16_t *vd = reinterpret_cast<uint16_t *>(vc) + ((nblk_id * Hkv + kvh) * D + 2 * lane) * BS + off;
-          vd[0] = static_cast<uint16_t>(nv & 0xffffu);
-          vd[BS] = static_cast<uint16_t>(nv >> 16);
-        }
-      }
-    }
-  }
-  float l = st.l + __shfl_xor(st.l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  // Merge the W waves through LDS into this chunk's partial (slot npp + chunk).
-  __shared__ float sm_o[W][16][D];
-  __shared__ float sm_m[W][16], sm_l[W][16];
-  if (col < G) {
-#pragma unroll
-    for (int n = 0; n < D / 16; ++n) *reinterpret_cast<floatx4 *>(&sm_o[wave][col][16 * n + 4 * grp]) = st.o[n];
-    if (grp == 0) {
-      sm_m[wave][col] = st.m;
-      sm_l[wave][col] = l;
-    }
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < G * D; e += 64 * W) {
-    const int h = e / D, d = e % D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w][h]);
-    const float m_use = (M == -INFINITY) ? 0.f : M;
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const float f = exp2f(sm_m[w][h] - m_use);
-      num += f * sm_o[w][h][d];
-      den += f * sm_l[w][h];
-    }
-    const int64_t prow = (static_cast<int64_t>(b) * Hq + kvh * G + h) * slots + gg.npp + chunk;
-    part_o[prow * D + d] = num;
-    if (d == 0) {
-      part_ml[2 * prow] = M;
-      part_ml[2 * prow + 1] = den;
-    }
-  }
-}
-
-// Slots of a grouped decode's partials: the prefix partitions' [0, n_pre) and
-// the suffix chunks' [npp, npp + n_suf), counted exactly as the kernel above
-// cuts them; every row is merged.
-struct GroupSlots {
-  GroupGeom gg;
-  const int32_t *seq_lens;
-  int max_seq, batch, BS, chunk_tokens;  // chunk_tokens = W * P_tok
-  __device__ bool operator()(int b, int &n0, int &s1, int &n1) const {
-    const int pre = group_prefix(gg, seq_lens, b / gg.gs, batch, max_seq, BS);
-    int L = seq_lens[b];
-    L = L < max_seq ? L : max_seq;
-    n0 = 0;
-    if (pre > 0) {
-      const int ppart = prefix_partition(pre, gg.p_pre, BS);
-      n0 = (pre + ppart - 1) / ppart;
-    }
-    s1 = gg.npp;
-    n1 = L > pre ? (L - pre + chunk_tokens - 1) / chunk_tokens : 0;
-    return true;
-  }
-};
-
 // Tokens per partition when the caller leaves it to the library: about 2,048
 // partition waves over the longest context -- every CU's resident slots in
 // about one round, and no more (fewer, longer waves amortise the per-wave
@@ -665,18 +436,63 @@ namespace wkv {
 // context length, longest first, ties by index -- rank(i) = #{j : L_j > L_i,
 // or L_j = L_i and j < i} is a permutation. O(batch^2) compares, spread over
 // ceil(batch / 256) workgroups; 256 sequences take ~10 us, once per step.
+// With n_cls > 1 (GRPO groups of group_size consecutive sequences; every class
+// holds batch / n_cls sequences), group g belongs to class g % n_cls, each
+// class is ranked longest first on its own, and rank r of class c is
+// dispatched at position r * n_cls + c: every member of a group then lands at
+// the same position modulo n_cls, which is what places a group's workgroups of
+// one KV head on one XCD (see grouped_order_classes).
+template <bool CLASSES>
 __global__ __launch_bounds__(256) void decode_order_kernel(const int32_t *__restrict__ seq_lens, int batch,
-                                                           int32_t *__restrict__ order) {
+                                                           int32_t *__restrict__ order, int group_size, int n_cls) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int ki = i < batch ? seq_lens[i] : 0;
   int rank = 0;
-  // every lane reads the same length: scalar loads, eight at a time
+  if constexpr (!CLASSES) {
+    // every lane reads the same length: scalar loads, eight at a time
 #pragma unroll 8
-  for (int j = 0; j < batch; ++j) {
-    const int kj = seq_lens[j];
-    rank += (kj > ki || (kj == ki && j < i)) ? 1 : 0;
+    for (int j = 0; j < batch; ++j) {
+      const int kj = seq_lens[j];
+      rank += (kj > ki || (kj == ki && j < i)) ? 1 : 0;
+    }
+    if (i < batch) order[rank] = i;
+  } else {
+    const int ci = (i / group_size) % n_cls;
+    // the class of sequence j is tracked incrementally (no division per step)
+    int cj = 0, in_group = 0;
+#pragma unroll 8
+    for (int j = 0; j < batch; ++j) {
+      const int kj = seq_lens[j];
+      rank += (cj == ci && (kj > ki || (kj == ki && j < i))) ? 1 : 0;
+      if (++in_group == group_size) {
+        in_group = 0;
+        cj = cj + 1 == n_cls ? 0 : cj + 1;
+      }
+    }
+    if (i < batch) order[rank * n_cls + ci] = i;
   }
-  if (i < batch) order[rank] = i;
+}
+
+// Workgroups are dispatched to the XCDs round-robin by linear workgroup id, and
+// each XCD has its own L2. A decode workgroup (chunk, KV head, rank) has linear
+// id chunk + chunks * (kvh + Hkv * rank), so the workgroups of ranks congruent
+// modulo 8 / gcd(8, chunks * Hkv) run on the same XCDs, head by head: the
+// number of order classes that keep a group's reads of its prompt in one L2.
+// 1 (plain longest-first order) when the classes would not be of equal size.
+constexpr int kXcds = 8;
+
+static int grouped_order_classes(int batch, int group_size, int hkv, int max_seq, int BS, int partition_size) {
+  const int P = partition_size != 0 ? partition_size : choose_partition(batch, hkv, max_seq, BS);
+  int W, chunks;
+  decode_shape(max_seq, P, &W, &chunks);
+  int a = chunks * hkv % kXcds, g = kXcds;  // gcd(kXcds, chunks * hkv)
+  while (a != 0) {
+    const int t = g % a;
+    g = a;
+    a = t;
+  }
+  const int n_cls = kXcds / g;
+  return batch % (group_size * n_cls) == 0 ? n_cls : 1;
 }
 
 static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stride_b, int64_t q_stride_h, void *out,
@@ -684,7 +500,8 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
                          int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch, int32_t max_seq_len,
                          float scale, int32_t partition_size, void *workspace, int64_t workspace_bytes,
                          const StepAppend *ap, const int32_t *seq_order, void *stream,
-                         bool static_scratch = false, const float *sinks = nullptr) {
+                         bool static_scratch = false, const float *sinks = nullptr,
+                         const int32_t *prefix_lens = nullptr, int group_size = 1, int max_prefix = 0) {
   int rc = check_cache(cache, -1);
   if (rc) return rc;
   WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
@@ -737,7 +554,9 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
   const StepAppend none{nullptr, 0, 0, nullptr, 0, 0, nullptr};
   const StepAppend apv = ap ? *ap : none;
-  const bool stream_reads = (cache->flags & WKV_CACHE_SHARED_BLOCKS) == 0;
+  // Groups: the shared prompt cached, each member's own tokens streamed (per sequence, in the kernel).
+  const int rp = prefix_lens != nullptr ? kReadSplit
+                                        : ((cache->flags & WKV_CACHE_SHARED_BLOCKS) == 0 ? kReadStreamed : kReadCached);
 #define WKV_DECODE_S(Dv, F8, AP, Wv, ST)                                                                         \
   decode_gqa_kernel<Dv, F8, AP, Wv, ST><<<grid, 64 * Wv, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, qq,     \
                                                                  q_stride_b, q_stride_h, oo, part_o, part_ml,    \
@@ -745,13 +564,15 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
                                                                  max_seq, seq_lens, seq_order,                   \
                                                                  num_q_heads, Hkv, G, BS, cache->num_blocks,     \
                                                                  scale_log2, partition_size, max_chunks, apv,    \
-                                                                 sinks)
-#define WKV_DECODE(Dv, F8, AP, Wv)           \
-  do {                                       \
-    if (stream_reads)                        \
-      WKV_DECODE_S(Dv, F8, AP, Wv, true);    \
-    else                                     \
-      WKV_DECODE_S(Dv, F8, AP, Wv, false);   \
+                                                                 sinks, prefix_lens, group_size, max_prefix)
+#define WKV_DECODE(Dv, F8, AP, Wv)                     \
+  do {                                                 \
+    if (rp == kReadStreamed)                           \
+      WKV_DECODE_S(Dv, F8, AP, Wv, kReadStreamed);     \
+    else if (rp == kReadCached)                        \
+      WKV_DECODE_S(Dv, F8, AP, Wv, kReadCached);       \
+    else                                               \
+      WKV_DECODE_S(Dv, F8, AP, Wv, kReadSplit);        \
   } while (0)
 #define WKV_DECODE_W(Dv, F8, AP)   \
   do {                             \
@@ -789,146 +610,13 @@ static int launch_decode(const wkv_cache_t *cache, const void *q, int64_t q_stri
   return WKV_OK;
 }
 
-// Grouped decode: the prefix role's workgroups hold kGroupW waves (row tiles
-// of one or more partitions), the suffix role's as many partitions. (8 waves:
-// -9% per layer against 4 on 32 groups x 8 sequences of Qwen2.5-7B, fp8.)
-constexpr int kGroupW = 8;
-
-static int grouped_partition(int32_t partition_size, int batch, int hkv, int max_seq, int BS) {
-  return partition_size != 0 ? partition_size : choose_partition(batch, hkv, max_seq, BS);
-}
-
-// Most tokens per prefix partition: about what the longest suffix gives each
-// of its waves (prefix workgroups then last no longer than suffix ones), at
-// least an eighth of the prefix (few partials), in whole blocks, within [BS, P].
-static int64_t grouped_prefix_partition(int64_t max_seq, int64_t max_prefix, int64_t P, int64_t BS) {
-  const int64_t pre = max_prefix < max_seq ? max_prefix : max_seq;
-  int64_t p = (max_seq - pre + kGroupW - 1) / kGroupW;
-  const int64_t eighth = (pre + 7) / 8;
-  if (p < eighth) p = eighth;
-  p = (p + BS - 1) / BS * BS;
-  if (p > P) p = P;
-  if (p < BS) p = BS;
-  return p;
-}
-
-// Partial slots per (sequence, query head): prefix partitions, then suffix chunks.
-static void grouped_slots(int64_t max_seq, int64_t max_prefix, int64_t P, int64_t BS, int64_t *npp, int64_t *nsc,
-                          int64_t *p_pre) {
-  const int64_t pre = max_prefix < max_seq ? max_prefix : max_seq;
-  *p_pre = grouped_prefix_partition(max_seq, max_prefix, P, BS);
-  *npp = (pre + *p_pre - 1) / *p_pre;
-  *nsc = (max_seq + kGroupW * P - 1) / (kGroupW * P);
-  if (*nsc < 1) *nsc = 1;
-}
-
-static int launch_grouped(const wkv_cache_t *cache, const StepAppend *ap, const void *q, int64_t q_stride_b,
-                          int64_t q_stride_h, void *out, int32_t num_q_heads, const int32_t *block_table,
-                          int64_t bt_stride, int32_t max_blocks_per_seq, const int32_t *seq_lens, int32_t batch,
-                          int32_t max_seq_len, const int32_t *prefix_lens, int32_t group_size,
-                          int32_t max_prefix_len, float scale, int32_t partition_size, void *workspace,
-                          int64_t workspace_bytes, const int32_t *seq_order, void *stream) {
-  int rc = check_cache(cache, -1);
-  if (rc) return rc;
-  WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
-  if (batch == 0) return WKV_OK;
-  const int Hkv = cache->num_kv_heads, D = cache->head_dim, BS = cache->block_size;
-  WKV_CHECK_ARG(num_q_heads > 0 && num_q_heads % Hkv == 0, "num_q_heads %d must be a multiple of num_kv_heads %d",
-                num_q_heads, Hkv);
-  const int G = num_q_heads / Hkv;
-  if (G > 16) return fail(WKV_ERR_UNSUPPORTED, "query group size %d > 16 not supported", G);
-  WKV_CHECK_ARG(static_cast<int64_t>(batch) * num_q_heads < INT32_MAX - 4, "batch * num_q_heads too large");
-  WKV_CHECK_ARG(Hkv <= 65535, "num_kv_heads too large");
-  WKV_CHECK_ARG(cache->num_blocks * Hkv <= INT32_MAX, "num_blocks * num_kv_heads must be below 2^31");
-  WKV_CHECK_ARG(q != nullptr && aligned16(q), "q must be non-NULL and 16-byte aligned");
-  WKV_CHECK_ARG(q_stride_b >= 0 && q_stride_h >= 0 && q_stride_b % 8 == 0 && q_stride_h % 8 == 0,
-                "q strides must be non-negative multiples of 8");
-  WKV_CHECK_ARG(out != nullptr && aligned16(out), "out must be non-NULL and 16-byte aligned");
-  WKV_CHECK_ARG(block_table != nullptr && seq_lens != nullptr, "block_table / seq_lens is NULL");
-  WKV_CHECK_ARG(max_blocks_per_seq > 0 && bt_stride >= max_blocks_per_seq, "bad block table geometry");
-  WKV_CHECK_ARG(max_seq_len >= 0, "max_seq_len must be >= 0");
-  WKV_CHECK_ARG(std::isfinite(scale), "scale must be finite");
-  WKV_CHECK_ARG(prefix_lens != nullptr, "prefix_lens is NULL");
-  WKV_CHECK_ARG(group_size >= 1 && group_size <= batch, "group_size must be in [1, batch] (got %d)", group_size);
-  WKV_CHECK_ARG(max_prefix_len >= 0, "max_prefix_len must be >= 0");
-  const int max_seq = max_seq_len < max_blocks_per_seq * BS ? max_seq_len : max_blocks_per_seq * BS;
-  const int P = grouped_partition(partition_size, batch, Hkv, max_seq, BS);
-  WKV_CHECK_ARG(P >= 16 && P % BS == 0, "partition_size %d must be a positive multiple of block_size %d", P, BS);
-  WKV_CHECK_ARG(P / BS <= 64, "partition_size %d spans more than 64 blocks of %d tokens", P, BS);
-  const int n_groups = (batch + group_size - 1) / group_size;
-  int64_t npp, nsc, p_pre;
-  grouped_slots(max_seq, max_prefix_len, P, BS, &npp, &nsc, &p_pre);
-  const int64_t slots = npp + nsc;
-  GroupGeom gg;
-  gg.prefix_lens = prefix_lens;
-  gg.gs = group_size;
-  gg.nrt = (group_size * G + 15) / 16;
-  gg.rows_w = gg.nrt < kGroupW ? gg.nrt : kGroupW;
-  gg.nrtb = (gg.nrt + gg.rows_w - 1) / gg.rows_w;
-  gg.ppw = gg.nrt <= kGroupW ? kGroupW / gg.nrt : 1;
-  gg.p_pre = static_cast<int>(p_pre);
-  gg.npp = static_cast<int>(npp);
-  gg.npb = (gg.npp + gg.ppw - 1) / gg.ppw;
-  gg.nsc = static_cast<int>(nsc);
-  gg.append = ap != nullptr ? 1 : 0;
-  const int64_t n_pre = static_cast<int64_t>(n_groups) * Hkv * gg.nrtb * gg.npb;
-  const int64_t n_suf = static_cast<int64_t>(batch) * Hkv * gg.nsc;
-  WKV_CHECK_ARG(n_pre + n_suf <= INT32_MAX, "grouped decode grid too large");
-  gg.n_pre_wgs = static_cast<int>(n_pre);
-  const int64_t need = static_cast<int64_t>(batch) * num_q_heads * slots * (D + 2) * 4;
-  WKV_CHECK_ARG(workspace != nullptr && aligned16(workspace) && workspace_bytes >= need,
-                "workspace too small: need %lld bytes, got %lld", (long long)need, (long long)workspace_bytes);
-  float *part_o = static_cast<float *>(workspace);
-  float *part_ml = part_o + static_cast<int64_t>(batch) * num_q_heads * slots * D;
-  const float scale_log2 = scale * 1.4426950408889634f;
-  auto s = static_cast<hipStream_t>(stream);
-  auto kc = static_cast<uint8_t *>(cache->k);
-  auto vc = static_cast<uint8_t *>(cache->v);
-  auto qq = static_cast<const uint16_t *>(q);
-  const bool fp8 = cache->kv_dtype == WKV_KV_FP8_E4M3;
-  const StepAppend none{nullptr, 0, 0, nullptr, 0, 0, nullptr};
-  const StepAppend apv = ap ? *ap : none;
-  const dim3 grid(static_cast<unsigned>(n_pre + n_suf));
-#define WKV_GROUPED(Dv, F8, AP)                                                                                 \
-  decode_gqa_grouped_kernel<Dv, F8, AP, kGroupW><<<grid, 64 * kGroupW, 0, s>>>(                                \
-      kc, vc, cache->k_scale, cache->v_scale, qq, q_stride_b, q_stride_h, part_o, part_ml, block_table,         \
-      bt_stride, max_blocks_per_seq, max_seq, seq_lens, seq_order, batch, num_q_heads, Hkv, G, BS,              \
-      cache->num_blocks, scale_log2, P, apv, gg)
-  if (D == 128) {
-    if (fp8) { if (ap) WKV_GROUPED(128, true, true); else WKV_GROUPED(128, true, false); }
-    else { if (ap) WKV_GROUPED(128, false, true); else WKV_GROUPED(128, false, false); }
-  } else {
-    if (fp8) { if (ap) WKV_GROUPED(64, true, true); else WKV_GROUPED(64, true, false); }
-    else { if (ap) WKV_GROUPED(64, false, true); else WKV_GROUPED(64, false, false); }
-  }
-#undef WKV_GROUPED
-  WKV_CHECK_LAUNCH("grouped paged decode");
-  auto oo = static_cast<uint16_t *>(out);
-  const int rows = batch * num_q_heads;
-  const GroupSlots gs{gg, seq_lens, max_seq, batch, BS, kGroupW * P};
-  if (D == 128)
-    merge_partials_kernel<128><<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads,
-                                                              static_cast<int>(slots), gs, nullptr);
-  else
-    merge_partials_kernel<64><<<(rows + 3) / 4, 256, 0, s>>>(part_o, part_ml, oo, rows, num_q_heads,
-                                                             static_cast<int>(slots), gs, nullptr);
-  WKV_CHECK_LAUNCH("grouped paged decode merge");
-  return WKV_OK;
-}
-
 }  // namespace wkv
 
 extern "C" int64_t wkv_grouped_decode_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim,
                                                      int32_t max_seq_len, int32_t max_prefix_len,
                                                      int32_t partition_size) {
-  if (batch < 0 || num_q_heads <= 0 || head_dim <= 0 || max_seq_len < 0 || max_prefix_len < 0 || partition_size < 0)
-    return -1;
-  // The smallest partition the library picks by itself, and the smallest block
-  // (both give the most slots).
-  if (partition_size == 0) partition_size = 128;
-  int64_t npp, nsc, p_pre;
-  wkv::grouped_slots(max_seq_len, max_prefix_len, partition_size, 16, &npp, &nsc, &p_pre);
-  return static_cast<int64_t>(batch) * num_q_heads * (npp + nsc) * (head_dim + 2) * 4;
+  if (max_prefix_len < 0) return -1;
+  return wkv_decode_workspace_size(batch, num_q_heads, head_dim, max_seq_len, partition_size);
 }
 
 extern "C" int wkv_paged_decode_gqa_grouped(const wkv_cache_t *cache, const void *key, int64_t key_stride_t,
@@ -942,6 +630,11 @@ extern "C" int wkv_paged_decode_gqa_grouped(const wkv_cache_t *cache, const void
                                             void *workspace, int64_t workspace_bytes, const int32_t *seq_order,
                                             void *stream) {
   using namespace wkv;
+  WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
+  if (batch == 0) return WKV_OK;
+  WKV_CHECK_ARG(prefix_lens != nullptr, "prefix_lens is NULL");
+  WKV_CHECK_ARG(group_size >= 1 && group_size <= batch, "group_size must be in [1, batch] (got %d)", group_size);
+  WKV_CHECK_ARG(max_prefix_len >= 0, "max_prefix_len must be >= 0");
   StepAppend ap{};
   const bool append = key != nullptr || value != nullptr || slot_mapping != nullptr;
   if (append) {
@@ -951,20 +644,45 @@ extern "C" int wkv_paged_decode_gqa_grouped(const wkv_cache_t *cache, const void
                       (key_stride_t | key_stride_h | value_stride_t | value_stride_h) % 8 == 0,
                   "key/value strides must be non-negative multiples of 8");
     WKV_CHECK_ARG(slot_mapping != nullptr, "slot_mapping is NULL");
+    if (cache != nullptr && cache->kv_dtype == WKV_KV_FP8_E4M3)
+      WKV_CHECK_ARG(cache->k_scale && cache->v_scale, "fp8 cache needs k_scale and v_scale");
     ap = StepAppend{static_cast<const uint16_t *>(key), key_stride_t, key_stride_h,
                     static_cast<const uint16_t *>(value), value_stride_t, value_stride_h, slot_mapping};
   }
-  return launch_grouped(cache, append ? &ap : nullptr, q, q_stride_b, q_stride_h, out, num_q_heads, block_table,
-                        bt_stride, max_blocks_per_seq, seq_lens, batch, max_seq_len, prefix_lens, group_size,
-                        max_prefix_len, scale, partition_size, workspace, workspace_bytes, seq_order, stream);
+  return launch_decode(cache, q, q_stride_b, q_stride_h, out, num_q_heads, block_table, bt_stride,
+                       max_blocks_per_seq, seq_lens, batch, max_seq_len, scale, partition_size, workspace,
+                       workspace_bytes, append ? &ap : nullptr, seq_order, stream, false, nullptr, prefix_lens,
+                       group_size, max_prefix_len);
 }
 
 extern "C" int wkv_decode_order(const int32_t *seq_lens, int32_t batch, int32_t *order, void *stream) {
   WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
   if (batch == 0) return WKV_OK;
   WKV_CHECK_ARG(seq_lens != nullptr && order != nullptr, "seq_lens / order is NULL");
-  decode_order_kernel<<<(batch + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(seq_lens, batch, order);
+  decode_order_kernel<false>
+      <<<(batch + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(seq_lens, batch, order, 1, 1);
   WKV_CHECK_LAUNCH("decode order");
+  return WKV_OK;
+}
+
+extern "C" int wkv_grouped_decode_order(const int32_t *seq_lens, int32_t batch, int32_t group_size,
+                                        int32_t num_kv_heads, int32_t max_seq_len, int32_t block_size,
+                                        int32_t partition_size, int32_t *order, void *stream) {
+  using namespace wkv;
+  WKV_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535] (got %d)", batch);
+  if (batch == 0) return WKV_OK;
+  WKV_CHECK_ARG(seq_lens != nullptr && order != nullptr, "seq_lens / order is NULL");
+  WKV_CHECK_ARG(group_size >= 1 && group_size <= batch, "group_size must be in [1, batch] (got %d)", group_size);
+  WKV_CHECK_ARG(num_kv_heads > 0 && max_seq_len >= 0 && partition_size >= 0, "bad decode geometry");
+  WKV_CHECK_ARG(block_size > 0 && block_size % 16 == 0, "block_size must be a positive multiple of 16");
+  const int n_cls = grouped_order_classes(batch, group_size, num_kv_heads, max_seq_len, block_size, partition_size);
+  if (n_cls == 1)
+    decode_order_kernel<false>
+        <<<(batch + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(seq_lens, batch, order, 1, 1);
+  else
+    decode_order_kernel<true><<<(batch + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        seq_lens, batch, order, group_size, n_cls);
+  WKV_CHECK_LAUNCH("grouped decode order");
   return WKV_OK;
 }
 

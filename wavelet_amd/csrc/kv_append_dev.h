@@ -19,6 +19,51 @@ __device__ __forceinline__ int64_t fp8_v_index(int64_t blk, int h, int H, int BS
   return ((blk * H + h) * D + d) * BS + off;
 }
 
+// Re-encodes the codes at offsets [0, first) of the (blk, h) region of K (IS_V
+// false) or V at a grown scale: each code times `ratio`, an exact power of two
+// below 1 (e4m3_encode(e4m3_decode(c) * ratio), code by code, as the oracle
+// states it). The region is walked in 16-byte pieces, four per lane a pass,
+// every load of a pass issued before its stores (a byte loop waits one memory
+// round trip per byte). K [D/16][BS][16]: piece p holds token p % BS's 16
+// d-values of one chunk; V [D][BS]: piece p holds tokens 16 (p % (BS/16)) ..
+// + 15 of one d row. Pieces at or past `first` are not stored.
+template <int D, bool IS_V>
+__device__ __forceinline__ void fp8_reencode_block(uint8_t *__restrict__ cache, int64_t blk, int h, int H, int BS,
+                                                   int first, float ratio) {
+  const int lane = threadIdx.x & 63;
+  u32x4 *base = reinterpret_cast<u32x4 *>(cache + (blk * H + h) * static_cast<int64_t>(D) * BS);
+  const int np = D * BS / 16;
+  constexpr int PL = 4;
+  for (int p0 = 0; p0 < np; p0 += 64 * PL) {
+    u32x4 w[PL];
+#pragma unroll
+    for (int k = 0; k < PL; ++k) {
+      const int p = p0 + 64 * k + lane;
+      if (p < np) w[k] = base[p];
+    }
+#pragma unroll
+    for (int k = 0; k < PL; ++k) {
+      const int p = p0 + 64 * k + lane;
+      const int tok0 = IS_V ? 16 * (p % (BS / 16)) : p % BS;
+      if (p >= np || tok0 >= first) continue;
+      u32x4 o = w[k];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int tok = IS_V ? tok0 + 4 * j + b : tok0;
+          if (tok < first) {
+            const uint32_t c = (o[j] >> (8 * b)) & 0xffu;
+            const uint32_t n = e4m3_encode(e4m3_decode(c) * ratio);
+            o[j] = (o[j] & ~(0xffu << (8 * b))) | (n << (8 * b));
+          }
+        }
+      }
+      base[p] = o;
+    }
+  }
+}
+
 template <int D, bool IS_V>
 __device__ void fp8_append_one(uint8_t *__restrict__ cache, float *__restrict__ scales,
                                const uint16_t *__restrict__ src, int64_t st, int64_t sh,
@@ -37,6 +82,10 @@ __device__ void fp8_append_one(uint8_t *__restrict__ cache, float *__restrict__ 
     const float s_old = scales[blk * H + h];
     s = (s_new > s_old) ? s_new : s_old;
     if (s > s_old) {
+      // Byte by byte: with fp8_reencode_block here the fused decode kernel that
+      // inlines this (one run of one token) measured 3-4% slower per launch
+      // even in steps where no block grows (fp8 Qwen2.5-7B groups and Qwen3-4B
+      // shapes, in-process A/B).
       const float ratio = s_old / s;  // exact power of two
       for (int e = lane; e < first * D; e += 64) {
         const int off = e / D, d = e % D;
@@ -82,12 +131,7 @@ __device__ void fp8_append_run_vec(uint8_t *__restrict__ cache, float *__restric
     const float s_old = scales[blk * H + h];
     s = (s_new > s_old) ? s_new : s_old;
     if (s > s_old) {  // the block's earlier codes are re-encoded at the grown scale
-      const float ratio = s_old / s;  // exact power of two
-      for (int e = lane; e < first * D; e += 64) {
-        const int off = e / D, d = e % D;
-        const int64_t a = IS_V ? fp8_v_index<D>(blk, h, H, BS, off, d) : fp8_k_index<D>(blk, h, H, BS, off, d);
-        cache[a] = static_cast<uint8_t>(e4m3_encode(e4m3_decode(cache[a]) * ratio));
-      }
+      fp8_reencode_block<D, IS_V>(cache, blk, h, H, BS, first, s_old / s);  // exact power-of-two ratio
     }
   }
   const float inv = 1.0f / s;  // exact: s is a power of two in [2^-42, 2^119]

@@ -128,17 +128,24 @@ __global__ __launch_bounds__(64) void append_fp8_kernel(uint8_t *__restrict__ kc
   fp8_append_one<D, true>(vc, vs, val, vst, vsh, slots, t, r, blk, first, h, H, BS);
 }
 
-// Bulk fp8 append (prompt-sized calls): one wave per (64-token window of the
-// call, KV head). The wave finds the runs that start in its window and their
-// lengths from ballots over the blocks of this window's and the next window's
-// tokens (a run lies in one block, so with blocks of at most 64 tokens it ends
-// within the next window), and appends each run -- K and V, with the same
-// scale rule; a run that reaches past the window is still this wave's. A whole
-// fresh 16-token block (the prompt case) takes fp8_append_block16: 16-byte
-// loads and stores, hardware code conversion. Other runs: fp8_append_run_vec.
+// Bulk fp8 append (calls of 64 tokens or more): one workgroup per (64-token
+// window of the call, KV head). Its waves find the runs that start in the
+// window and their lengths from ballots over the blocks of this window's and
+// the next window's tokens (a run lies in one block, so with blocks of at most
+// 64 tokens it ends within the next window); wave w appends the window's runs
+// w, w + kFp8BulkWaves, ... -- K and V, with the same scale rule; a run that
+// reaches past the window is still this window's. Runs are independent (a block
+// is in at most one run of a call), so the waves need no synchronisation: a
+// window of four 16-token prompt blocks takes four waves side by side, and a
+// decode-shaped call (one token per sequence: 64 runs of one token per window)
+// eight runs per wave instead of 64.
+// A whole fresh 16-token block (the prompt case) takes fp8_append_block16:
+// 16-byte loads and stores, hardware code conversion. Other runs:
+// fp8_append_run_vec.
 constexpr int kFp8BulkMinTokens = 64;
+constexpr int kFp8BulkWaves = 8;
 template <int D>
-__global__ __launch_bounds__(64) void append_fp8_bulk_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
+__global__ __launch_bounds__(64 * kFp8BulkWaves) void append_fp8_bulk_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
                                                              float *__restrict__ ks, float *__restrict__ vs,
                                                              const uint16_t *__restrict__ key, int64_t kst,
                                                              int64_t ksh, const uint16_t *__restrict__ val,
@@ -147,7 +154,8 @@ __global__ __launch_bounds__(64) void append_fp8_bulk_kernel(uint8_t *__restrict
                                                              int BS, int64_t NB) {
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
   const int h = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   // block of token `tok` of the call (-1: past the call, a skipped slot or an
   // unmapped block); block ids are below 2^31 (num_blocks * num_kv_heads is)
   auto block_of = [&](int64_t tok) -> int {
@@ -168,9 +176,10 @@ __global__ __launch_bounds__(64) void append_fp8_bulk_kernel(uint8_t *__restrict
   const bool start = ba >= 0 && pa != ba;
   uint64_t starts = __ballot(start);
   const uint64_t ca = __ballot(ba >= 0 && pa == ba), cb = __ballot(bb >= 0 && pb == bb);
-  while (starts != 0ull) {  // uniform
+  for (int k = 0; starts != 0ull; ++k) {  // uniform
     const int i = __ffsll(static_cast<long long>(starts)) - 1;
     starts &= starts - 1ull;
+    if (k % kFp8BulkWaves != wave) continue;  // another wave's run
     const int64_t t = t0 + i;
     const int64_t slot = slots[t];
     const int64_t blk = slot / BS;
@@ -433,13 +442,13 @@ extern "C" int wkv_append_fp8(const wkv_cache_t *cache, const void *key, int64_t
   if (num_tokens >= kFp8BulkMinTokens && rows16) {
     const dim3 bgrid(static_cast<unsigned>((num_tokens + 63) / 64), static_cast<unsigned>(H));
     if (D == 128)
-      append_fp8_bulk_kernel<128><<<bgrid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
-                                                        key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
-                                                        num_tokens, H, cache->block_size, cache->num_blocks);
+      append_fp8_bulk_kernel<128><<<bgrid, 64 * kFp8BulkWaves, 0, s>>>(
+          kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t, key_stride_h, v, value_stride_t, value_stride_h,
+          slot_mapping, num_tokens, H, cache->block_size, cache->num_blocks);
     else
-      append_fp8_bulk_kernel<64><<<bgrid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
-                                                       key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
-                                                       num_tokens, H, cache->block_size, cache->num_blocks);
+      append_fp8_bulk_kernel<64><<<bgrid, 64 * kFp8BulkWaves, 0, s>>>(
+          kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t, key_stride_h, v, value_stride_t, value_stride_h,
+          slot_mapping, num_tokens, H, cache->block_size, cache->num_blocks);
   } else if (D == 128)
     append_fp8_kernel<128><<<grid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
                                                key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,

@@ -80,13 +80,14 @@ class DecodeStep:
     With ``group_size`` and ``prefix_lens`` (int32 ``[n_groups]`` on the device)
     the attention is the group-aware one (``paged_decode_gqa_grouped``): GRPO
     groups of ``group_size`` consecutive sequences read their shared prompt
-    blocks once per group; ``max_prefix_len`` bounds ``prefix_lens``.
+    blocks through the caches and their own tokens streamed; ``max_prefix_len``
+    bounds ``prefix_lens``.
 
     With ``order_by_length``, ``run`` first computes the step's dispatch order
-    (``decode_order``: longest contexts first, one launch shared by every
-    layer) and each layer's decode dispatches its sequences (the group-aware
-    decode: the members' own tokens) in that order; the results are the same
-    bit for bit. ``None`` (the default) orders
+    (``decode_order``: longest contexts first; for groups ``grouped_decode_order``,
+    which also keeps a group's members on one XCD; one launch shared by every
+    layer) and each layer's decode dispatches its sequences in that order; the
+    results are the same bit for bit. ``None`` (the default) orders
     when ``B * Hkv * max_seq_len >= 2**20``: below that a launch is short
     enough (~50 us) that the order's dependent read at each workgroup's start
     costs more than mixed lengths lose. Calling ``step_layer`` / ``attend``
@@ -98,7 +99,8 @@ class DecodeStep:
     the step is read by more than one sequence (K/V reads keep it cached for
     the next reader), False to stream every block (``KVPool.decode_shares_blocks``
     computes it from the block manager's reference counts once per step). The
-    group-aware decode chooses its own policy per role.
+    group-aware decode sets its own: each group's prompt cached, the members' own
+    tokens streamed.
     """
 
     def __init__(self, caches: list[PagedKVCache], q: list[torch.Tensor], key: list[torch.Tensor],
@@ -119,6 +121,7 @@ class DecodeStep:
         lib = _lib.load()
         hq = q[0].shape[1]
         self.grouped = group_size > 0
+        self.group_size = int(group_size)
         if self.grouped:
             n_groups = -(-batch // group_size)
             if (prefix_lens is None or prefix_lens.dtype != torch.int32 or tuple(prefix_lens.shape) != (n_groups,)
@@ -178,8 +181,15 @@ class DecodeStep:
         """Compute this step's dispatch order from ``seq_lens`` (one launch)."""
         self._live.check_all()
         if self.ordered:
-            rc = self.lib.wkv_decode_order(self.seq_lens.data_ptr(), self.seq_lens.shape[0], self.order.data_ptr(),
-                                           self.stream)
+            if self.grouped:
+                c0 = self._keep[0][0]
+                rc = self.lib.wkv_grouped_decode_order(
+                    self.seq_lens.data_ptr(), self.seq_lens.shape[0], self.group_size, c0.num_kv_heads,
+                    min(self.max_seq_len, self.block_table.shape[1] * c0.block_size), c0.block_size,
+                    self.partition_size, self.order.data_ptr(), self.stream)
+            else:
+                rc = self.lib.wkv_decode_order(self.seq_lens.data_ptr(), self.seq_lens.shape[0],
+                                               self.order.data_ptr(), self.stream)
             if rc:
                 _lib.check(rc, "decode order")
 
