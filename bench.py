@@ -122,6 +122,7 @@ TRAFFIC_PROFILES = {
     ("qwen3-4b-var", "bf16"): "profiles/decode_gqa_qwen3_4b_var_pmc.md",
     ("qwen2.5-0.5b", "bf16"): "profiles/decode_gqa_qwen2_5_0_5b_pmc.md",
     ("deepseek-v3-mla", "bf16"): "profiles/decode_mla_deepseek_v3.md",
+    ("qwen2.5-7b-groups", "fp8_e4m3"): "profiles/decode_gqa_fp8_groups.md",
 }
 
 

@@ -6,9 +6,10 @@ Every plan here is built by the benchmark's own constructor calls
 library's partition, dispatch order and waves per workgroup) on two layers of
 the full-size workload, so the kernel instantiations and launch shapes under
 test are the ones the bench line reports -- e.g. the headline's
-``decode_gqa_kernel<128,false,true,8,true>`` (streamed reads) with 512-token
+``decode_gqa_kernel<128,false,true,8,1>`` (streamed reads) with 512-token
 partitions and one workgroup per (sequence, KV head), no merge, and the fp8
-groups' kernels with the cached read policy of shared prompt blocks.
+groups' kernels: the group-aware one (prompt blocks cached, the members' own
+tokens streamed, the group order) and the plain one (everything cached).
 
 Per layer, after one ``run()``:
 

@@ -279,3 +279,63 @@ def test_append_gather_matches_golden_digests(cuda, golden_dir):
     gk, gv = cache.gather(torch.from_numpy(w.block_tables).to(cuda), torch.from_numpy(w.context_lens).to(cuda))
     assert synth.sha256_of(bits_of(gk)) == expected["gathered_k"]
     assert synth.sha256_of(bits_of(gv)) == expected["gathered_v"]
+
+
+def _fp8_case(cuda, NB, BS, H, D):
+    kc, vc = paged.empty_cache(NB, BS, H, D, dtype=np.uint8, fill=0xAA)
+    ks = np.zeros((NB, H), np.float32)
+    vs = np.zeros((NB, H), np.float32)
+    cache = PagedKVCache(NB, BS, H, D, kv_dtype="fp8_e4m3", device=cuda)
+    _upload(cache, kc, vc, ks, vs)
+
+    def both(key_bits, val_bits, slots, what):
+        paged.append_fp8(kc, vc, ks, vs, key_bits, val_bits, slots)
+        cache.append(to_dev_bits(key_bits, BF16, cuda), to_dev_bits(val_bits, BF16, cuda),
+                     torch.from_numpy(np.asarray(slots, np.int64)).to(cuda))
+        _assert_cache_equal(cache, kc, vc, ks, vs, what=what)
+    return both
+
+
+def test_append_fp8_decode_shaped_call(cuda):
+    """One token per sequence (a decode step's append, 256 one-token runs in scattered,
+    partly filled blocks; most scales grow and re-encode the block's earlier codes): the
+    bulk kernel's many-runs-per-window case, bit-exact codes and scales."""
+    NB, BS, H, D = 512, 16, 4, 128
+    rng = np.random.default_rng(11)
+    both = _fp8_case(cuda, NB, BS, H, D)
+    blocks = rng.permutation(NB)[:256]
+    fill = rng.integers(1, BS, 256)
+    prior = np.concatenate([b * BS + np.arange(f) for b, f in zip(blocks, fill)]).astype(np.int64)
+    both(synth.normal_bf16(synth.stream_key("fp8dec", "k0"), (len(prior), H, D), std=0.05),
+         synth.normal_bf16(synth.stream_key("fp8dec", "v0"), (len(prior), H, D), std=0.05), prior, "contexts")
+    step = (blocks * BS + fill).astype(np.int64)
+    step[::17] = -1  # sequences without a token this step
+    both(synth.normal_bf16(synth.stream_key("fp8dec", "k1"), (256, H, D), std=2.0),
+         synth.normal_bf16(synth.stream_key("fp8dec", "v1"), (256, H, D), std=0.01), step, "decode step")
+
+
+@pytest.mark.parametrize("BS", [16, 32])
+def test_append_fp8_prompt_sized_call(cuda, BS):
+    """A prompt-sized call (4,096 tokens or more: the bulk kernel's prompt launch shape):
+    several prompts in shuffled blocks, one continuing a partly filled block, one ending in a
+    partial block -- bit-exact codes and scales."""
+    NB, H, D = 1024 // (BS // 16), 2, 128
+    rng = np.random.default_rng(BS + 3)
+    both = _fp8_case(cuda, NB, BS, H, D)
+    blocks = rng.permutation(NB)
+    head = (blocks[0] * BS + np.arange(5)).astype(np.int64)  # a block already holding 5 tokens
+    both(synth.normal_bf16(synth.stream_key("fp8pr", BS, "k0"), (64, H, D), std=0.01),
+         synth.normal_bf16(synth.stream_key("fp8pr", BS, "v0"), (64, H, D), std=0.01),
+         np.concatenate([head, np.full(59, -1)]), "a partly filled block")
+    lens = [BS - 5 + 7 * BS, 1500, 1111, 1000, 700]  # the first continues blocks[0]
+    slots = [np.concatenate([blocks[0] * BS + np.arange(5, BS), blocks[1:8].repeat(BS) * BS + np.tile(np.arange(BS), 7)])]
+    nb = 8
+    for L in lens[1:]:
+        k = (L + BS - 1) // BS
+        own = blocks[nb:nb + k]
+        nb += k
+        slots.append((own.repeat(BS) * BS + np.tile(np.arange(BS), k))[:L])
+    s = np.concatenate(slots).astype(np.int64)
+    assert len(s) >= 4096
+    both(synth.normal_bf16(synth.stream_key("fp8pr", BS, "k1"), (len(s), H, D), std=1.0),
+         synth.normal_bf16(synth.stream_key("fp8pr", BS, "v1"), (len(s), H, D), std=3.0), s, "prompts")

@@ -128,24 +128,27 @@ __global__ __launch_bounds__(64) void append_fp8_kernel(uint8_t *__restrict__ kc
   fp8_append_one<D, true>(vc, vs, val, vst, vsh, slots, t, r, blk, first, h, H, BS);
 }
 
-// Bulk fp8 append (calls of 64 tokens or more): one workgroup per (64-token
-// window of the call, KV head). Its waves find the runs that start in the
-// window and their lengths from ballots over the blocks of this window's and
-// the next window's tokens (a run lies in one block, so with blocks of at most
-// 64 tokens it ends within the next window); wave w appends the window's runs
-// w, w + kFp8BulkWaves, ... -- K and V, with the same scale rule; a run that
-// reaches past the window is still this window's. Runs are independent (a block
-// is in at most one run of a call), so the waves need no synchronisation: a
-// window of four 16-token prompt blocks takes four waves side by side, and a
-// decode-shaped call (one token per sequence: 64 runs of one token per window)
-// eight runs per wave instead of 64.
-// A whole fresh 16-token block (the prompt case) takes fp8_append_block16:
-// 16-byte loads and stores, hardware code conversion. Other runs:
-// fp8_append_run_vec.
+// Bulk fp8 append (calls of 64 tokens or more): one workgroup of NW waves per
+// (64-token window of the call, KV head). Its waves find the runs that start
+// in the window and their lengths from ballots over the blocks of this
+// window's and the next window's tokens (a run lies in one block, so with
+// blocks of at most 64 tokens it ends within the next window); wave w appends
+// the window's runs w, w + NW, ... -- K and V, with the same scale rule; a run
+// that reaches past the window is still this window's. Runs are independent (a
+// block is in at most one run of a call), so the waves need no
+// synchronisation. A decode-shaped call (one token per sequence: 64 one-token
+// runs per window) takes NW = 8: 256 tokens x 4 heads 58 us against 318 with
+// one wave per window; a prompt (four 16-token blocks per window) NW = 4, one
+// block per wave: 16,384 tokens x 8 heads 23.5 us (one wave per window 23.9,
+// eight 30.1; kernel traces). A whole fresh 16-token block (the prompt case) takes
+// fp8_append_block16: 16-byte loads and stores, hardware code conversion.
+// Other runs: fp8_append_run_vec.
 constexpr int kFp8BulkMinTokens = 64;
-constexpr int kFp8BulkWaves = 8;
-template <int D>
-__global__ __launch_bounds__(64 * kFp8BulkWaves) void append_fp8_bulk_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
+// Calls of this many tokens or more are taken as prompts (NW = 4), smaller
+// ones as decode-shaped (NW = 8).
+constexpr int64_t kFp8PromptTokens = 4096;
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void append_fp8_bulk_kernel(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
                                                              float *__restrict__ ks, float *__restrict__ vs,
                                                              const uint16_t *__restrict__ key, int64_t kst,
                                                              int64_t ksh, const uint16_t *__restrict__ val,
@@ -179,7 +182,7 @@ __global__ __launch_bounds__(64 * kFp8BulkWaves) void append_fp8_bulk_kernel(uin
   for (int k = 0; starts != 0ull; ++k) {  // uniform
     const int i = __ffsll(static_cast<long long>(starts)) - 1;
     starts &= starts - 1ull;
-    if (k % kFp8BulkWaves != wave) continue;  // another wave's run
+    if (k % NW != wave) continue;  // another wave's run
     const int64_t t = t0 + i;
     const int64_t slot = slots[t];
     const int64_t blk = slot / BS;
@@ -441,14 +444,18 @@ extern "C" int wkv_append_fp8(const wkv_cache_t *cache, const void *key, int64_t
                       value_stride_t % 8 == 0 && value_stride_h % 8 == 0;
   if (num_tokens >= kFp8BulkMinTokens && rows16) {
     const dim3 bgrid(static_cast<unsigned>((num_tokens + 63) / 64), static_cast<unsigned>(H));
-    if (D == 128)
-      append_fp8_bulk_kernel<128><<<bgrid, 64 * kFp8BulkWaves, 0, s>>>(
-          kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t, key_stride_h, v, value_stride_t, value_stride_h,
-          slot_mapping, num_tokens, H, cache->block_size, cache->num_blocks);
-    else
-      append_fp8_bulk_kernel<64><<<bgrid, 64 * kFp8BulkWaves, 0, s>>>(
-          kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t, key_stride_h, v, value_stride_t, value_stride_h,
-          slot_mapping, num_tokens, H, cache->block_size, cache->num_blocks);
+#define WKV_FP8_BULK(Dv, NWv)                                                                                   \
+  append_fp8_bulk_kernel<Dv, NWv><<<bgrid, 64 * NWv, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k,         \
+                                                             key_stride_t, key_stride_h, v, value_stride_t,    \
+                                                             value_stride_h, slot_mapping, num_tokens, H,      \
+                                                             cache->block_size, cache->num_blocks)
+    const bool prompt = num_tokens >= kFp8PromptTokens;
+    if (D == 128) {
+      if (prompt) WKV_FP8_BULK(128, 4); else WKV_FP8_BULK(128, 8);
+    } else {
+      if (prompt) WKV_FP8_BULK(64, 4); else WKV_FP8_BULK(64, 8);
+    }
+#undef WKV_FP8_BULK
   } else if (D == 128)
     append_fp8_kernel<128><<<grid, 64, 0, s>>>(kc, vc, cache->k_scale, cache->v_scale, k, key_stride_t,
                                                key_stride_h, v, value_stride_t, value_stride_h, slot_mapping,
