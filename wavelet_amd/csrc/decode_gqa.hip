@@ -144,8 +144,8 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
         if (slot >= 0 && slot / BS < NB) {
           const int64_t blk = slot / BS;
           const int off = static_cast<int>(slot % BS);
-          fp8_append_one<D, false>(kc, ks, ap.key, ap.kst, ap.ksh, ap.slots, b, 1, blk, off, kvh, Hkv, BS);
-          fp8_append_one<D, true>(vc, vs, ap.val, ap.vst, ap.vsh, ap.slots, b, 1, blk, off, kvh, Hkv, BS);
+          fp8_append_token_kv<D>(kc, vc, ks, vs, ap.key + b * ap.kst + kvh * ap.ksh, ap.val + b * ap.vst + kvh * ap.vsh,
+                                 blk, off, kvh, Hkv, BS);
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
       } else {

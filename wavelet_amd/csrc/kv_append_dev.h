@@ -104,6 +104,67 @@ __device__ void fp8_append_one(uint8_t *__restrict__ cache, float *__restrict__ 
   if (lane == 0) scales[blk * H + h] = s;
 }
 
+// fp8 append of one token (the fused decode's step token) for one head, K and
+// V together: both source rows and both old scales are loaded at once and
+// both rows reduced side by side, so the two appends cost one chain of memory
+// round trips instead of two. The same codes, scales and re-encodes as
+// fp8_append_one on each of K and V with a run of one token.
+template <int D>
+__device__ __forceinline__ void fp8_append_token_kv(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
+                                                    float *__restrict__ ks, float *__restrict__ vs,
+                                                    const uint16_t *__restrict__ krow,
+                                                    const uint16_t *__restrict__ vrow, int64_t blk, int off, int h,
+                                                    int H, int BS) {
+  constexpr int PER = D / 64;  // elements of a row per lane: d = lane + 64 i
+  const int lane = threadIdx.x & 63;
+  float xk[PER], xv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    xk[i] = bf16_bits_to_f32(krow[lane + 64 * i]);
+    xv[i] = bf16_bits_to_f32(vrow[lane + 64 * i]);
+  }
+  const int64_t si = blk * H + h;
+  const float sk_old = off != 0 ? ks[si] : 0.f, sv_old = off != 0 ? vs[si] : 0.f;
+  float ak = 0.f, av = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    ak = fmaxf(ak, fabsf(xk[i]));
+    av = fmaxf(av, fabsf(xv[i]));
+  }
+  ak = wave_max(ak);
+  av = wave_max(av);
+  float sk = pow2_scale(ak), sv = pow2_scale(av);
+  if (off != 0) {
+    if (sk > sk_old) {  // the block's earlier K codes at the grown scale, byte by byte
+      const float ratio = sk_old / sk;
+      for (int e = lane; e < off * D; e += 64) {
+        const int64_t a = fp8_k_index<D>(blk, h, H, BS, e / D, e % D);
+        kc[a] = static_cast<uint8_t>(e4m3_encode(e4m3_decode(kc[a]) * ratio));
+      }
+    } else {
+      sk = sk_old;
+    }
+    if (sv > sv_old) {
+      const float ratio = sv_old / sv;
+      for (int e = lane; e < off * D; e += 64) {
+        const int64_t a = fp8_v_index<D>(blk, h, H, BS, e / D, e % D);
+        vc[a] = static_cast<uint8_t>(e4m3_encode(e4m3_decode(vc[a]) * ratio));
+      }
+    } else {
+      sv = sv_old;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    kc[fp8_k_index<D>(blk, h, H, BS, off, lane + 64 * i)] = static_cast<uint8_t>(e4m3_quantize(xk[i], sk));
+    vc[fp8_v_index<D>(blk, h, H, BS, off, lane + 64 * i)] = static_cast<uint8_t>(e4m3_quantize(xv[i], sv));
+  }
+  if (lane == 0) {
+    ks[si] = sk;
+    vs[si] = sv;
+  }
+}
+
 // The same append with 16-byte source loads and 16-byte K stores, and the
 // quantisation as a product with 1 / scale (a power of two: x * (1 / s) and
 // x / s round the same exact value, so the codes are identical). The source
