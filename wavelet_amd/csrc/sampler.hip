@@ -268,6 +268,9 @@ constexpr int kMassBins = 711;
 constexpr int kMaskWords = 8192;
 // Draws a wave may hold back before making them 64 at a time (final pass).
 constexpr int kQueue = 128;
+// The same for the final pass's fast loop, which makes its draws after every
+// fourth token slot: fewer than 64 pending, plus 64 per slot.
+constexpr int kFastQueue = 64 + 4 * 64;
 static_assert(kBins == 2 * kSampleThreads, "the threshold scan gives every thread two bins");
 
 __device__ __forceinline__ unsigned long long fixed_mass(float x, float mx) {
@@ -301,6 +304,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   __shared__ uint32_t fcnt[kBins];
   __shared__ unsigned long long fmass[kBins];  // also the final pass's draw queues
   static_assert(sizeof(fmass) >= (kSampleThreads / 64) * kQueue * 8, "the draw queues fit the mass bins");
+  __shared__ float fq_x[kSampleThreads / 64][kFastQueue];  // the fast loop's draw queues (value, token)
+  __shared__ int32_t fq_t[kSampleThreads / 64][kFastQueue];
   __shared__ uint32_t ckey[kCand];
   __shared__ float cx[kCand];
   __shared__ int32_t cidx[kCand];
@@ -810,6 +815,63 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     lz = static_cast<float>(log(static_cast<double>(ztot)) - 22.180709777918249);  // - ln 2^32
     if (a.mask)
       for (int wd = tid; wd < words; wd += kSampleThreads) a.mask[static_cast<int64_t>(b) * words + wd] = mbits[wd];
+  } else if (!greedy && key_lo < 0x80000000u) {
+    // Final pass over the row, fast loop: the keep threshold is a negative
+    // float t (the RL defaults keep every finite token, and most min_p rows
+    // land here). Keys order negative floats (-0 included) as the floats do
+    // and every non-negative float above them, and NaN fails both compares as
+    // it fails the key test, so: kept <=> v >= t, and a race candidate (kept
+    // and v >= lim) <=> v >= max(t, lim), one float compare each. The draws go
+    // through a queue per wave, made 64 at a time after every fourth token
+    // slot (lim only moves there): the token slots in between carry no draw
+    // code, and the mass, counts and mask come out as in the general loop.
+    const float thr = __uint_as_float(~key_lo);
+    float clim = fmaxf(thr, lim);
+    float *qx = &fq_x[tid >> 6][0];
+    int32_t *qt = &fq_t[tid >> 6][0];
+    int qn = 0;  // wave-uniform
+    float z = 0.f;
+    for_chunks(Every{}, [&](const float v[kVec], int64_t base) {
+      uint32_t bits = 0;
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) {
+        const bool kept = v[j] >= thr;
+        if (__ballot(kept) != 0ull) {  // uniform: something kept in this slot of the wave
+          if (kept) {
+            bits |= 1u << j;
+            z += __expf(v[j] - mx);
+          }
+          const bool c = v[j] >= clim;
+          const unsigned long long bal = __ballot(c);
+          if (bal != 0ull) {  // uniform
+            if (c) {
+              const int at = qn + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                      static_cast<uint32_t>(bal >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+              qx[at] = v[j];
+              qt[at] = static_cast<int32_t>(base) + j;
+            }
+            qn += __popcll(bal);
+          }
+        }
+        if ((j & 3) == 3) {
+          while (qn >= 64) {  // uniform
+            qn -= 64;
+            race(qx[qn + lane], qt[qn + lane]);
+          }
+          clim = fmaxf(thr, lim);
+        }
+      }
+      cnt += __popc(bits);
+      if (a.mask) {
+        // four consecutive lanes hold the 32 bits of one mask word
+        const uint32_t b1 = __shfl_down(bits, 1, 64), b2 = __shfl_down(bits, 2, 64), b3 = __shfl_down(bits, 3, 64);
+        const int64_t wd = base >> 5;
+        if ((tid & 3) == 0 && wd < words)
+          a.mask[static_cast<int64_t>(b) * words + wd] = bits | (b1 << 8) | (b2 << 16) | (b3 << 24);
+      }
+    });
+    if (lane < qn) race(qx[lane], qt[lane]);
+    lz = logf(block_sum(z, redv));
   } else {
     // Final pass over the row. Every lane makes the same calls (chunks past
     // the end are all -inf, kept nowhere): the mask words below are assembled
