@@ -436,7 +436,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
   };
   // Appends the kept tokens with `take` set to the list (one LDS atomic per
   // wave and slot); every lane of the wave that is still in the pass calls it.
-  auto append = [&](bool take, uint32_t k, float x, int64_t t) {
+  auto append = [&](bool take, float x, int64_t t) {
     const unsigned long long bal = __ballot(take);
     if (bal == 0ull) return;  // uniform: most slots of most passes
     const int first = __ffsll(static_cast<long long>(bal)) - 1;
@@ -445,7 +445,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     at = __shfl(at, first, 64) + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
     if (take && at < kCand) {
-      ckey[at] = k;
+      ckey[at] = order_key(x);
       cx[at] = x;
       cidx[at] = static_cast<int32_t>(t);
     }
@@ -503,33 +503,50 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
     const bool captured = bcap < kBins - 1;
     if (captured) {
       unsigned long long tmass = 0;
-      // (one instance per mass flag: a select on it would compute every mass)
-      auto capture = [&](auto with_mass) {
+      // The bin tests as distance compares: with d = (mx - x) * kBinScale as
+      // bin_of forms it (d >= 0: x <= mx; NaN and -inf fail every compare),
+      // bin <= bcap <=> d < bcap + 1 and bin < kMassBins <=> d < kMassBins
+      // (bcap + 1 <= kBins - 1). The key test is one float compare when the
+      // threshold is a negative float (NEG; see the fast final loop below).
+      // The bin and the key are formed only for the few tokens taken.
+      const float bcap1 = static_cast<float>(bcap + 1);
+      const float thr = __uint_as_float(~key_lo);  // with NEG: the keep threshold as a float
+      // (one instance per mass flag and key test: a select on them would do both)
+      auto capture = [&](auto with_mass, auto neg) {
         constexpr bool M = decltype(with_mass)::value;
+        constexpr bool NEG = decltype(neg)::value;
         for_chunks(Own{}, [&](const float v[kVec], int64_t base) {
 #pragma unroll
           for (int j = 0; j < kVec; ++j) {
-            const uint32_t k = order_key(v[j]);
-            const int bn = bin_of(v[j]);
-            const bool kept = k >= key_lo;
+            const float d = (mx - v[j]) * kBinScale;
+            const bool kept = NEG ? v[j] >= thr : order_key(v[j]) >= key_lo;
             unsigned long long m = 0;
             if constexpr (M) {
-              if (kept && bn < kMassBins) m = fixed_mass(v[j], mx);
+              if (kept && d < static_cast<float>(kMassBins)) m = fixed_mass(v[j], mx);
               tmass += m;
             }
-            const bool take = kept && bn <= bcap;
+            const bool take = kept && d < bcap1;
             if (take) {
+              const int bn = static_cast<int>(d);
               atomicAdd(&fcnt[bn], 1u);
               if constexpr (M) atomicAdd(&fmass[bn], m);
             }
-            append(take, k, v[j], base + j);
+            append(take, v[j], base + j);
           }
         });
       };
-      if (hmass)
-        capture(std::true_type{});
-      else
-        capture(std::false_type{});
+      const bool neg_thr = key_lo < 0x80000000u;
+      if (hmass) {
+        if (neg_thr)
+          capture(std::true_type{}, std::true_type{});
+        else
+          capture(std::true_type{}, std::false_type{});
+      } else {
+        if (neg_thr)
+          capture(std::false_type{}, std::true_type{});
+        else
+          capture(std::false_type{}, std::false_type{});
+      }
       if (hmass) {
         const unsigned long long wm = wave_sum_u64(tmass);
         if (lane == 0) atomicAdd(&sel_n, wm);
@@ -614,10 +631,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const T *__restr
       if (!fallback) {
         for_chunks(Own{}, [&](const float v[kVec], int64_t base) {
 #pragma unroll
-          for (int j = 0; j < kVec; ++j) {
-            const uint32_t k = order_key(v[j]);
-            append(k >= key_lo && bin_of(v[j]) <= tb, k, v[j], base + j);
-          }
+          for (int j = 0; j < kVec; ++j) append(order_key(v[j]) >= key_lo && bin_of(v[j]) <= tb, v[j], base + j);
         });
         __syncthreads();
         n = ncand < kCand ? ncand : kCand;  // == n_list
