@@ -56,8 +56,10 @@ __device__ __forceinline__ float sink_weight(const float *sinks, int hq, float m
 //     partition start, so the tiles, and the result, are the plain call's.
 constexpr int kReadCached = 0, kReadStreamed = 1, kReadSplit = 2;
 
+// fp8: held to 128 VGPRs (four waves per SIMD, as before the fused append's
+// tile patch, which took the grouped instances to 130 and three waves).
 template <int D, bool FP8, bool APPEND, int W, int RP>
-__global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(FP8 ? 4 : 1))) void decode_gqa_kernel(
     uint8_t *__restrict__ kc, uint8_t *__restrict__ vc, float *__restrict__ ks, float *__restrict__ vs,
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ out,
     float *__restrict__ part_o, float *__restrict__ part_ml, const int32_t *__restrict__ bt, int64_t bt_stride,
@@ -96,6 +98,16 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     load_q<D, FP8>(qop, q + b * q_sb + static_cast<int64_t>(kvh * G + (col < G ? col : 0)) * q_sh, col < G, grp);
   }
 
+  // fp8 fused append: the step token's slot and K/V rows go out now, with the
+  // loads above (every wave: which one appends is known only from the
+  // length); the appending wave's chain then starts at the old scales.
+  int64_t slot_pre = -1;
+  Fp8TokenRows<D> rows_pre;
+  if constexpr (APPEND && FP8) {
+    slot_pre = ap.slots[b];
+    fp8_token_rows_load<D>(rows_pre, ap.key + b * ap.kst + kvh * ap.ksh, ap.val + b * ap.vst + kvh * ap.vsh);
+  }
+
   // The group's shared prompt: tokens [0, cut), read with the default policy.
   int cut = 0;
   if constexpr (RP == kReadSplit) {
@@ -130,25 +142,52 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
 
   // Fused append; the new token's block lies wholly in this wave's partition
   // (the partition size is a multiple of the block size): no other wave reads it.
-  // fp8: a scale change can re-encode the whole block, so append first and
-  //      wait before the block is read back.
+  // fp8: when the slot is the table's position L - 1 and the block's scales
+  //      do not grow, the token's codes and the block's scales enter the tile
+  //      that holds it in registers, exactly as a read of the cache after
+  //      the append would bring them (so the output is the unfused call's),
+  //      and the codes (and a new block's scales) are written after the
+  //      tiles: stores count in the wave's in-order vmcnt, so written first
+  //      they held up every tile load behind them (measured per fp8 Qwen3-4B
+  //      layer: 92.9 -> 88.8 us). Otherwise (a scale grows and re-encodes the
+  //      block, or the slot lies elsewhere) append first and wait before the
+  //      block is read.
   // bf16: the wave attends the cache up to the new token and then the token
   //      itself from the step's inputs (held one dword per lane), writing it
   //      to the cache at the end; nothing waits on the write or the slot.
   uint32_t nk = 0, nv = 0;
   int64_t slot = -1;
+  __shared__ uint8_t tok_code[(APPEND && FP8) ? W : 1][2][D];  // the fp8 token's K and V codes, per wave
+  int patch_ts = -1, patch_p = 0;  // the tile holding the fp8 token, its row in the tile
+  float psk = 1.f, psv = 1.f;      // the block's scales after the append
+  bool late = false;               // the fp8 token's writes wait for the end
   if constexpr (APPEND) {
     if (owns_new) {
-      slot = ap.slots[b];
       if constexpr (FP8) {
+        slot = slot_pre;
         if (slot >= 0 && slot / BS < NB) {
           const int64_t blk = slot / BS;
           const int off = static_cast<int>(slot % BS);
-          fp8_append_token_kv<D>(kc, vc, ks, vs, ap.key + b * ap.kst + kvh * ap.ksh, ap.val + b * ap.vst + kvh * ap.vsh,
-                                 blk, off, kvh, Hkv, BS);
+          const int tbl = __builtin_amdgcn_readlane(my_blk, (L - 1) / BS - blk_first);
+          const Fp8TokenCodes<D> cd = fp8_token_codes<D>(ks, vs, rows_pre, blk, off, kvh, Hkv);
+          if (tbl == blk && off == (L - 1) % BS && !cd.grow) {  // uniform
+            late = true;
+            psk = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cd.sk)));  // uniform: scalar registers
+            psv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cd.sv)));
+#pragma unroll
+            for (int i = 0; i < D / 64; ++i) {
+              tok_code[wave][0][lane + 64 * i] = static_cast<uint8_t>(cd.k[i]);
+              tok_code[wave][1][lane + 64 * i] = static_cast<uint8_t>(cd.v[i]);
+            }
+            patch_ts = t_begin + 16 * (((L - 1) - t_begin) >> 4);
+            patch_p = (L - 1) - patch_ts;
+          } else {
+            fp8_append_token_kv<D>(kc, vc, ks, vs, rows_pre, blk, off, kvh, Hkv, BS);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+          }
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
       } else {
+        slot = ap.slots[b];
         if (lane < D / 2) {
           nk = reinterpret_cast<const uint32_t *>(ap.key + b * ap.kst + kvh * ap.ksh)[lane];
           nv = reinterpret_cast<const uint32_t *>(ap.val + b * ap.vst + kvh * ap.vsh)[lane];
@@ -166,24 +205,70 @@ __global__ __launch_bounds__(64 * W) void decode_gqa_kernel(
     const int t_end = (t_begin + P_seq) < L ? (t_begin + P_seq) : L;
     const bool from_regs = APPEND && !FP8 && owns_new;  // last token comes from the inputs
     const int te = from_regs ? L - 1 : t_end;
+    // Each tile, as loaded; the fp8 token's tile first takes the token's codes
+    // (K: row patch_p of the tile, the lanes holding that token; V: byte
+    // patch_p of every lane's d row) and the block's scales after the append.
+    auto consume = [&](Tile<D, FP8> &t) __attribute__((always_inline)) {
+      if constexpr (APPEND && FP8) {
+        if (t.ts == patch_ts) {  // uniform; never for the other waves (-1)
+          const uint32_t sh = 8u * static_cast<uint32_t>(patch_p & 3);
+#pragma unroll
+          for (int j = 0; j < Tile<D, FP8>::NK; ++j) {
+            // dword by dword: one register of the tile loop's budget, not four
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const uint32_t kw = *reinterpret_cast<const uint32_t *>(&tok_code[wave][0][16 * (4 * j + grp) + 4 * w]);
+              if (col == patch_p) t.k[j][w] = kw;
+            }
+            const uint32_t vq = tok_code[wave][1][lane + 64 * j];
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+              if (w == (patch_p >> 2)) t.v4[j][w] = (t.v4[j][w] & ~(0xffu << sh)) | (vq << sh);
+          }
+          t.ksc = psk;
+          t.vsc = psv;
+        }
+      }
+      attend_tile<D, FP8>(st, t, qop, scale_log2, grp);
+    };
+    auto attend = [&](int mb, int t0, int t1, bool stream) __attribute__((always_inline)) {
+      attend_range<D, FP8>(consume, kc, vc, ks, vs, mb, t0, t1, kvh, Hkv, BS, NB, lane, col, grp, stream);
+    };
     if constexpr (RP == kReadSplit) {
       // [t_begin, c) of the shared prompt cached, [c, te) streamed; c - t_begin is
       // a multiple of 16, so both ranges hold the partition's own 16-token tiles.
       int c = cut - t_begin;
       c = t_begin + (c > 0 ? (c & ~15) : 0);
-      if (c > t_begin)
-        attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, te < c ? te : c, kvh, Hkv, BS, NB,
-                                 scale_log2, lane, col, grp, false);
+      if (c > t_begin) attend(my_blk, t_begin, te < c ? te : c, false);
       if (te > c) {
         // the streamed range's block ids, lane i = its i-th block
         const int sh = c / BS - blk_first;
         const int mb = sh > 0 ? __shfl(my_blk, (lane + sh) & 63, 64) : my_blk;
-        attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, mb, c, te, kvh, Hkv, BS, NB, scale_log2, lane, col, grp,
-                                 true);
+        attend(mb, c, te, true);
       }
     } else {
-      attend_partition<D, FP8>(st, kc, vc, ks, vs, qop, my_blk, t_begin, te, kvh, Hkv, BS, NB, scale_log2, lane,
-                               col, grp, RP == kReadStreamed);
+      attend(my_blk, t_begin, te, RP == kReadStreamed);
+    }
+    if constexpr (APPEND && FP8) {
+      if (late) {  // the token's codes (staged by this wave above) and the block's scales
+        const int64_t blk = slot / BS;
+        const int off = static_cast<int>(slot % BS);
+        if (col == 0) {
+#pragma unroll
+          for (int j = 0; j < Tile<D, FP8>::NK; ++j)
+            *reinterpret_cast<u32x4 *>(kc + fp8_k_index<D>(blk, kvh, Hkv, BS, off, 16 * (4 * j + grp))) =
+                *reinterpret_cast<const u32x4 *>(&tok_code[wave][0][16 * (4 * j + grp)]);
+        }
+#pragma unroll
+        for (int i = 0; i < D / 64; ++i)
+          vc[fp8_v_index<D>(blk, kvh, Hkv, BS, off, lane + 64 * i)] = tok_code[wave][1][lane + 64 * i];
+        // A block's scales change only with its first token here (a growing
+        // scale takes the append-first path): otherwise they are already stored.
+        if (off == 0 && lane == 0) {
+          ks[blk * Hkv + kvh] = psk;
+          vs[blk * Hkv + kvh] = psv;
+        }
+      }
     }
     if constexpr (APPEND && !FP8) {
       if (owns_new) {

@@ -104,24 +104,91 @@ __device__ void fp8_append_one(uint8_t *__restrict__ cache, float *__restrict__ 
   if (lane == 0) scales[blk * H + h] = s;
 }
 
+// The step token's K and V rows of one head as loaded (bf16 bits, d = lane +
+// 64 i): loaded apart from the rest of the append so that a caller can issue
+// them early and let their round trip overlap its own start (nothing here
+// waits for them; the append below converts them).
+template <int D>
+struct Fp8TokenRows {
+  uint32_t k[D / 64], v[D / 64];
+};
+template <int D>
+__device__ __forceinline__ void fp8_token_rows_load(Fp8TokenRows<D> &r, const uint16_t *__restrict__ krow,
+                                                    const uint16_t *__restrict__ vrow) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    r.k[i] = krow[lane + 64 * i];
+    r.v[i] = vrow[lane + 64 * i];
+  }
+}
+
+// The step token's codes and the block's scales after its append, without
+// writing anything: the same scale decision as fp8_append_token_kv (the
+// token's power-of-two scale, or the block's own if that is not smaller),
+// `grow` when the block's earlier codes would need re-encoding, and the
+// token's K and V codes at the resulting scales, d = lane + 64 i.
+template <int D>
+struct Fp8TokenCodes {
+  uint32_t k[D / 64], v[D / 64];
+  float sk, sv;
+  bool grow;
+};
+template <int D>
+__device__ __forceinline__ Fp8TokenCodes<D> fp8_token_codes(const float *__restrict__ ks, const float *__restrict__ vs,
+                                                            const Fp8TokenRows<D> &rows, int64_t blk, int off, int h,
+                                                            int H) {
+  constexpr int PER = D / 64;
+  float xk[PER], xv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    xk[i] = bf16_bits_to_f32(static_cast<uint16_t>(rows.k[i]));
+    xv[i] = bf16_bits_to_f32(static_cast<uint16_t>(rows.v[i]));
+  }
+  const int64_t si = blk * H + h;
+  const float sk_old = off != 0 ? ks[si] : 0.f, sv_old = off != 0 ? vs[si] : 0.f;
+  float ak = 0.f, av = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    ak = fmaxf(ak, fabsf(xk[i]));
+    av = fmaxf(av, fabsf(xv[i]));
+  }
+  ak = wave_max(ak);
+  av = wave_max(av);
+  Fp8TokenCodes<D> c;
+  c.sk = pow2_scale(ak);
+  c.sv = pow2_scale(av);
+  c.grow = false;
+  if (off != 0) {
+    c.grow = c.sk > sk_old || c.sv > sv_old;
+    if (!(c.sk > sk_old)) c.sk = sk_old;
+    if (!(c.sv > sv_old)) c.sv = sv_old;
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    c.k[i] = e4m3_quantize(xk[i], c.sk);
+    c.v[i] = e4m3_quantize(xv[i], c.sv);
+  }
+  return c;
+}
+
 // fp8 append of one token (the fused decode's step token) for one head, K and
-// V together: both source rows and both old scales are loaded at once and
+// V together, from its loaded rows: both old scales are loaded at once and
 // both rows reduced side by side, so the two appends cost one chain of memory
 // round trips instead of two. The same codes, scales and re-encodes as
 // fp8_append_one on each of K and V with a run of one token.
 template <int D>
 __device__ __forceinline__ void fp8_append_token_kv(uint8_t *__restrict__ kc, uint8_t *__restrict__ vc,
                                                     float *__restrict__ ks, float *__restrict__ vs,
-                                                    const uint16_t *__restrict__ krow,
-                                                    const uint16_t *__restrict__ vrow, int64_t blk, int off, int h,
-                                                    int H, int BS) {
+                                                    const Fp8TokenRows<D> &rows, int64_t blk, int off, int h, int H,
+                                                    int BS) {
   constexpr int PER = D / 64;  // elements of a row per lane: d = lane + 64 i
   const int lane = threadIdx.x & 63;
   float xk[PER], xv[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    xk[i] = bf16_bits_to_f32(krow[lane + 64 * i]);
-    xv[i] = bf16_bits_to_f32(vrow[lane + 64 * i]);
+    xk[i] = bf16_bits_to_f32(static_cast<uint16_t>(rows.k[i]));
+    xv[i] = bf16_bits_to_f32(static_cast<uint16_t>(rows.v[i]));
   }
   const int64_t si = blk * H + h;
   const float sk_old = off != 0 ? ks[si] : 0.f, sv_old = off != 0 ? vs[si] : 0.f;
