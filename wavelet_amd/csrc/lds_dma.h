@@ -31,6 +31,34 @@ __device__ __forceinline__ void buffer_copy16_to_lds(__amdgpu_buffer_rsrc_t r, u
                "s"(soff)
                : "memory", "m0");
 }
+// NCP copies of 1 KB under one M0 write: copy k lands at lds + 1024 k. The
+// LDS address of a copy is M0 + its instruction offset + 16 x lane, and the
+// instruction offset (1024 k here) is added to the memory address as well, so
+// the SGPR offset of copy k is k x sdelta with sdelta = (source stride of the
+// copies) - 1024. One M0 write per run instead of one per copy.
+template <int NCP>
+__device__ __forceinline__ void buffer_copy16_run_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t sdelta,
+                                                         uint32_t lds) {
+  static_assert(NCP >= 1 && NCP <= 4, "instruction offsets below 4096");
+  if constexpr (NCP == 1) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff),
+                 "s"(r)
+                 : "memory", "m0");
+  } else if constexpr (NCP == 2) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+                 "buffer_load_dwordx4 %1, %2, %3 offen offset:1024 lds" ::"s"(lds),
+                 "v"(voff), "s"(r), "s"(sdelta)
+                 : "memory", "m0");
+  } else {
+    const uint32_t s2 = 2 * sdelta, s3 = 3 * sdelta;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+                 "buffer_load_dwordx4 %1, %2, %3 offen offset:1024 lds\n\t"
+                 "buffer_load_dwordx4 %1, %2, %4 offen offset:2048 lds\n\t"
+                 "buffer_load_dwordx4 %1, %2, %5 offen offset:3072 lds" ::"s"(lds),
+                 "v"(voff), "s"(r), "s"(sdelta), "s"(s2), "s"(s3)
+                 : "memory", "m0");
+  }
+}
 #pragma clang diagnostic pop
 
 // Waits until at most N of this wave's vector-memory operations are pending.

@@ -62,9 +62,9 @@ struct LdsTile {
 //                                                 waits on itself)
 //   one row maximum, one rescale test            over the 64 keys
 //   P V^T                                        4 x D/32 MFMAs 32x32x16
-//   copies of the wave's tile: V of this step,  one buffer resource per
-//   K of the next                                 cache, 16-byte copies with a
-//                                                 uniform offset each
+//   copies of the wave's tile: V of the next     one buffer resource each,
+//   step, K of the step after                    16-byte copies (the K copies
+//                                                 under one M0)
 // so the per-step costs (barriers, waits, loop and mask tests, the maximum's
 // cross-lane swap) and the per-tile block lookup fall on 32 MFMAs. Row i of
 // each half's S^T carries key kperm(i) of the half (rows 4..7 and 8..11 of
@@ -73,19 +73,29 @@ struct LdsTile {
 // on the packed bf16 probabilities the PV products consume (v_dot2c_f32_bf16
 // against 1.0, two per instruction). A block id outside [0, num_blocks) reads block 0: no
 // access leaves the cache, and that sequence's output is unspecified.
-// LDS (bf16 caches): K in two step slots (the next step's K lands during
-// this step), V in one (a step's V is copied at its start and lands during
-// its QK and softmax; a second barrier per step separates the softmax from
-// the PV products): 48 KB at d=128, so three workgroups share a CU.
+//
+// Software pipeline, one workgroup barrier per step: while a wave finishes
+// step s (its probabilities, then its PV products) it scores step s + 1, so
+// its MFMAs and its softmax VALU work overlap inside the wave --
+//   phase A: the QK products of step s + 1  ||  exponentials, packing and row
+//            sum of step s
+//   phase B: the PV products of step s      ||  mask, exponents against the
+//            reference and their maximum of step s + 1 (the rare move of the
+//            reference maximum rescales after the PV products)
+// (interleaved by sched_group_barrier: an MFMA, then a few VALU, with the LDS
+// operand reads four MFMAs ahead). The copies of a step are one step ahead:
+// at the barrier of step s every wave's V of step s and K of step s + 1 have
+// landed and every wave is done with step s - 1, whose slots take V of step
+// s + 1 and K of step s + 2. LDS (bf16 tiles): K and V in two step slots
+// each, 64 KB at d=128, two workgroups per CU at up to 256 VGPRs per wave.
 // fp8 caches: the copies land in a staging area of the copying wave's own,
-// and that wave dequantizes its tile into the bf16 layout above with the
+// and that wave dequantizes its tiles into the bf16 layout above with the
 // hardware conversion at the (block, head) scale (a power of two: exact in
-// bf16) -- its V tile of this step before the first barrier, its K tile of
-// the next step after the PV products, into the single bf16 K slot every wave
-// has left at the first barrier. The attention arithmetic is the bf16 one.
-// LDS: 16 + 16 KB bf16 plus 8 + 8 KB staging at d=128.
+// bf16) after the wait and before the barrier of the step: its V tile of
+// step s and its K tile of step s + 1. The attention arithmetic is the bf16
+// one. LDS: 64 KB bf16 plus 8 + 8 KB staging at d=128.
 template <int D, bool FP8>
-__global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
+__global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_gqa_kernel(
     const uint8_t *__restrict__ kc, const uint8_t *__restrict__ vc, const float *__restrict__ ksc,
     const float *__restrict__ vsc, const uint16_t *__restrict__ q, int64_t q_st,
     int64_t q_sh, uint16_t *__restrict__ out, int64_t o_st, int64_t o_sh, const int32_t *__restrict__ cu_q,
@@ -99,12 +109,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
   constexpr int ESZ = FP8 ? 1 : 2;          // cache bytes per element
   constexpr int NC = D * 16 * ESZ / 1024;   // 16-byte copies per lane of a tile's K (and of its V)
   constexpr int DV = D / 64;                // bf16 V copies per token octet
-  constexpr int KSLOTS = FP8 ? 1 : 2;       // bf16 K step slots
   constexpr int SB = FP8 ? D * 16 : 16;     // fp8 staging bytes per tile, K or V
-  __shared__ __attribute__((aligned(16))) uint8_t ldsk[KSLOTS * 4 * KB];  // bf16 K: step slots of four tiles
-  __shared__ __attribute__((aligned(16))) uint8_t ldsv[4 * VB];           // bf16 V: one step
-  __shared__ __attribute__((aligned(16))) uint8_t stgk[4 * SB];           // fp8 K as copied, a tile per wave
-  __shared__ __attribute__((aligned(16))) uint8_t stgv[4 * SB];           // fp8 V as copied
+  __shared__ __attribute__((aligned(16))) uint8_t ldsk[2 * 4 * KB];  // bf16 K: two step slots of four tiles
+  __shared__ __attribute__((aligned(16))) uint8_t ldsv[2 * 4 * VB];  // bf16 V: two step slots
+  __shared__ __attribute__((aligned(16))) uint8_t stgk[4 * SB];      // fp8 K as copied, a tile per wave
+  __shared__ __attribute__((aligned(16))) uint8_t stgv[4 * SB];      // fp8 V as copied
   const int id = blockIdx.x;
   const int item = (id / (8 * n_qt)) * 8 + (id & 7);
   const int qt = __builtin_amdgcn_readfirstlane(n_qt - 1 - (id / 8) % n_qt);
@@ -152,6 +161,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
   const int n_tiles = kend > 0 ? (kend + 15) / 16 : 0;
   const int n_steps = (n_tiles + 3) / 4;
   const int region = D * BS * ESZ;
+  const int min_pos = ctx + t0;  // the smallest query position of the workgroup
 
   // Copy k of lane l moves piece p = 64 k + l of the wave's tile's K or V
   // (LDS offset 16 p). K piece p (both dtypes: 16-byte chunks): chunk p >> 4,
@@ -165,9 +175,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
   const uint32_t lane_v = static_cast<uint32_t>(lane * BS * ESZ);
   const uint32_t ldsk0 = lds_addr(ldsk), ldsv0 = lds_addr(ldsv);
   const uint32_t stgk0 = lds_addr(stgk), stgv0 = lds_addr(stgv);
-  float ks_next = 1.f, vs_next = 1.f, vs_cur = 1.f;  // fp8 scales of the wave's tiles
-  // This wave's tile of step s is tile 4 s + wave: token 64 s + 16 wave, in
-  // block bix at offset o0, both advanced by 64 tokens per step.
+  float ks_next = 1.f, vs_next = 1.f, vs_stage = 1.f;  // fp8 scales: last K issued, its V, the staged V
   const int32_t *btrow = bt + b * bt_stride;
   int bix = (16 * wave) / BS;
   int o0 = 16 * wave - bix * BS;
@@ -175,16 +183,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
   int wbase = 0;  // the window: lane i holds the id of block wbase + i
   int win = load_i32_drained(btrow, lane, Mb);
   int64_t vbase = 0;  // V of the wave's tile of the step whose K went out last: cache offset
-  // K of the wave's tile of step s into K slot `slot` (and its V offset kept for issue_v)
+  auto has_tile = [&](int s) { return s < n_steps && 4 * s + wave < n_tiles; };  // uniform
+  // K of the wave's tile of step s into K slot `slot` (fp8: into the staging area)
   auto issue_k = [&](int s, int slot) {
-    if (4 * s + wave < n_tiles) {  // uniform
-      if (bix - wbase >= 64) {     // at most once per 64 blocks (its wait drains the copies in flight)
+    if (has_tile(s)) {
+      if (bix - wbase >= 64) {  // at most once per 64 blocks (its wait drains the copies in flight)
         wbase += 64;
         win = load_i32_drained(btrow, wbase + lane, Mb);
       }
       int blk = __builtin_amdgcn_readlane(win, bix - wbase);
       if (!(blk >= 0 && blk < nb)) blk = 0;
-      // (block, head) region index < 2^31 (checked by the host), times the region
       const int64_t rb = static_cast<int64_t>(static_cast<uint64_t>(static_cast<uint32_t>(blk * Hkv + kvh)) *
                                               static_cast<uint32_t>(region));
       vbase = rb + o0 * ESZ;
@@ -192,15 +200,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
         ks_next = ksc[blk * Hkv + kvh];
         vs_next = vsc[blk * Hkv + kvh];
       }
-      // copy part of K copy k: 64 BS k (recomputed here, not held in registers)
+      // copy part of K copy k: 64 BS k = 1024 k (its LDS offset, the instruction
+      // offset) + k (64 BS - 1024)
       uint32_t kst = static_cast<uint32_t>(64 * BS);
       asm volatile("" : "+s"(kst));
       const __amdgpu_buffer_rsrc_t kr =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(kc + rb + o0 * 16), 0, region, kRawBufferWord3);
       const uint32_t dst = FP8 ? stgk0 + static_cast<uint32_t>(wave * SB)
                                : ldsk0 + static_cast<uint32_t>((4 * slot + wave) * KB);
-#pragma unroll
-      for (int k = 0; k < NC; ++k) buffer_copy16_to_lds(kr, lane_k, kst * k, dst + 1024 * k);
+      buffer_copy16_run_to_lds<NC>(kr, lane_k, kst - 1024u, dst);
     }
     o0 += do0;
     bix += dbix;
@@ -209,20 +217,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
       ++bix;
     }
   };
-  // V of the wave's tile of step s (whose K went out last) into the V slot
-  auto issue_v = [&](int s) {
-    if (4 * s + wave < n_tiles) {
+  // V of the wave's tile of step s (whose K went out last) into V slot `slot`
+  auto issue_v = [&](int s, int slot) {
+    if (has_tile(s)) {
       const __amdgpu_buffer_rsrc_t vr =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(vc + vbase), 0, region, kRawBufferWord3);
       if constexpr (FP8) {
+        vs_stage = vs_next;
         const uint32_t dst = stgv0 + static_cast<uint32_t>(wave * SB);
-        uint32_t vst = static_cast<uint32_t>(64 * BS);  // copy part: 64 BS k
+        uint32_t vst = static_cast<uint32_t>(64 * BS);
         asm volatile("" : "+s"(vst));
 #pragma unroll
         for (int k = 0; k < NC; ++k) buffer_copy16_to_lds(vr, lane_v, vst * k, dst + 1024 * k);
       } else {
-        const uint32_t dst = ldsv0 + static_cast<uint32_t>(wave * VB);
-        uint32_t vst = static_cast<uint32_t>(128 * BS);  // copy part: 128 BS (k % DV) + 16 (k / DV)
+        const uint32_t dst = ldsv0 + static_cast<uint32_t>((4 * slot + wave) * VB);
+        uint32_t vst = static_cast<uint32_t>(128 * BS);
         asm volatile("" : "+s"(vst));
 #pragma unroll
         for (int k = 0; k < NC; ++k)
@@ -230,197 +239,273 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 3) void prefill_gqa_kernel(
       }
     }
   };
-  // fp8: the wave's K tile, staged, into bf16 K slot 0 at scale sc. Piece
-  // p = 64 i + l: chunk c = p >> 4 (16 d), token m = p & 15 -> bf16 chunks
-  // 2c, 2c + 1 of token m.
-  auto convert_k = [&](float sc) {
+  // fp8: the wave's K tile, staged, into bf16 K slot `slot` at scale sc.
+  // Piece p = 64 i + l: chunk c = p >> 4 (16 d), token m = p & 15 -> bf16
+  // chunks 2c, 2c + 1 of token m.
+  auto convert_k = [&](float sc, int slot) {
 #pragma unroll
     for (int i = 0; i < D / 64; ++i) {
       const int pc = 64 * i + lane;
       const u32x4 w = *reinterpret_cast<const u32x4 *>(stgk + wave * SB + pc * 16);
-      uint8_t *dk = ldsk + wave * KB + ((2 * (pc >> 4)) * 16 + (pc & 15)) * 16;
+      uint8_t *dk = ldsk + (4 * slot + wave) * KB + ((2 * (pc >> 4)) * 16 + (pc & 15)) * 16;
       *reinterpret_cast<u32x4 *>(dk) = fp8x8_to_bf16_words(w[0], w[1], sc);
       *reinterpret_cast<u32x4 *>(dk + 256) = fp8x8_to_bf16_words(w[2], w[3], sc);
     }
   };
-  // fp8: the wave's V tile, staged, into the bf16 V slot at scale sc, tokens
-  // at or past vt zeroed. Piece p = 64 i + l: row p, 16 tokens -> octets 0, 1
-  // of row p.
-  auto convert_v = [&](float sc, int vt) {
+  // fp8: the wave's V tile, staged, into bf16 V slot `slot` at scale sc,
+  // tokens at or past vt zeroed (the slots past the keys may hold NaN). Piece
+  // p = 64 i + l: row p, 16 tokens -> octets 0, 1 of row p.
+  auto convert_v = [&](float sc, int vt, int slot) {
 #pragma unroll
     for (int i = 0; i < D / 64; ++i) {
       const int pc = 64 * i + lane;
       const u32x4 w = *reinterpret_cast<const u32x4 *>(stgv + wave * SB + pc * 16);
       u32x4 lo = fp8x8_to_bf16_words(w[0], w[1], sc), hi = fp8x8_to_bf16_words(w[2], w[3], sc);
-      if (vt < 16) {  // uniform: the tile's slots past the keys may hold NaN
+      if (vt < 16) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           if (e >= vt) lo[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
           if (8 + e >= vt) hi[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
         }
       }
-      *reinterpret_cast<u32x4 *>(ldsv + wave * VB + pc * 16) = lo;
-      *reinterpret_cast<u32x4 *>(ldsv + wave * VB + (D + pc) * 16) = hi;
+      uint8_t *dv = ldsv + (4 * slot + wave) * VB;
+      *reinterpret_cast<u32x4 *>(dv + pc * 16) = lo;
+      *reinterpret_cast<u32x4 *>(dv + (D + pc) * 16) = hi;
     }
   };
-  // Row n of each half's S^T carries key kperm(n) of the half.
+  // Step s's copies have landed (this wave's): make its V tile (and fp8: the
+  // next step's K tile) ready in the bf16 slots -- fp8 conversion, slots of a
+  // partial tile past the keys zeroed.
+  // Before the last step every wave's tile of step s is whole and its K tile
+  // of step s + 1 is converted whether or not it exists (a tile past the keys
+  // is masked): the fp8 conversion then runs without branches, its four LDS
+  // reads ahead of the conversions.
+  auto land_body = [&](int s) {
+    if constexpr (FP8) {
+      u32x4 wv[D / 64], wk[D / 64];
+#pragma unroll
+      for (int i = 0; i < D / 64; ++i) {
+        wv[i] = *reinterpret_cast<const u32x4 *>(stgv + wave * SB + (64 * i + lane) * 16);
+        wk[i] = *reinterpret_cast<const u32x4 *>(stgk + wave * SB + (64 * i + lane) * 16);
+      }
+      uint8_t *dv = ldsv + (4 * (s & 1) + wave) * VB;
+      uint8_t *dk = ldsk + (4 * ((s + 1) & 1) + wave) * KB;
+#pragma unroll
+      for (int i = 0; i < D / 64; ++i) {
+        const int pc = 64 * i + lane;
+        *reinterpret_cast<u32x4 *>(dv + pc * 16) = fp8x8_to_bf16_words(wv[i][0], wv[i][1], vs_stage);
+        *reinterpret_cast<u32x4 *>(dv + (D + pc) * 16) = fp8x8_to_bf16_words(wv[i][2], wv[i][3], vs_stage);
+        uint8_t *k = dk + ((2 * (pc >> 4)) * 16 + (pc & 15)) * 16;
+        *reinterpret_cast<u32x4 *>(k) = fp8x8_to_bf16_words(wk[i][0], wk[i][1], ks_next);
+        *reinterpret_cast<u32x4 *>(k + 256) = fp8x8_to_bf16_words(wk[i][2], wk[i][3], ks_next);
+      }
+    }
+  };
+  auto land = [&](int s) {
+    int vt = kend - 64 * s - 16 * wave;  // keys of this wave's tile of step s
+    vt = vt < 0 ? 0 : (vt > 16 ? 16 : vt);
+    if constexpr (FP8) {
+      if (vt > 0) convert_v(vs_stage, vt, s & 1);  // uniform
+      if (has_tile(s + 1)) convert_k(ks_next, (s + 1) & 1);
+    } else if (vt > 0 && vt < 16) {  // uniform; at most once per workgroup
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i) {
+        const int pc = 64 * i + lane;
+        const int cnt = vt - 8 * (pc / D);
+        u32x4 *ptr = reinterpret_cast<u32x4 *>(ldsv + (4 * (s & 1) + wave) * VB + pc * 16);
+        u32x4 w = *ptr;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (e >= cnt) w[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+        *ptr = w;
+      }
+    }
+  };
   const int kn = (n & 16) | (((n >> 2) & 3) == 1 ? (n & 3) + 8 : ((n >> 2) & 3) == 2 ? (n & 3) + 4 : (n & 15));
   const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+  uint32_t pw[4][4];  // PV B operands of the step being finished: packed bf16 probabilities
+
+  // S^T of step s (K slot s & 1) into (x0, x1)
+  auto qk = [&](int s, floatx16 &x0, floatx16 &x1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x0[r] = x1[r] = 0.f;
+    const uint8_t *lk = ldsk + ((s & 1) * 4 + (kn >> 4)) * KB + (kn & 15) * 16;
+#pragma unroll
+    for (int jj = 0; jj < D / 16; ++jj) {
+      const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + (2 * jj + hh) * 256));
+      const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + 2 * KB + (2 * jj + hh) * 256));
+      x0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qb[jj], x0, 0, 0, 0);
+      x1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qb[jj], x1, 0, 0, 0);
+    }
+  };
+  // causal / end mask of step s's scores
+  auto mask = [&](int s, floatx16 &x0, floatx16 &x1) {
+    const int kb = 64 * s;
+    if (!(kend >= kb + 64 && kb + 63 <= min_pos)) {  // uniform: masks in this step
+      const int pos = min_pos + n;
+      const int lim = (pos < kend - 1 ? pos : kend - 1) - kb - 8 * hh;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (16 * (r / 8) + (r % 8) > lim) x0[r] = -INFINITY;
+        if (32 + 16 * (r / 8) + (r % 8) > lim) x1[r] = -INFINITY;
+      }
+    }
+  };
+  // exponents against the reference maximum and their maximum
+  auto expo = [&](floatx16 &x0, floatx16 &x1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x0[r] = __builtin_fmaf(x0[r], scale_log2, -m_ref);
+      x1[r] = __builtin_fmaf(x1[r], scale_log2, -m_ref);
+    }
+    float mt0 = fmaxf(x0[0], x0[1]), mt1 = fmaxf(x1[0], x1[1]);
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) {
+      mt0 = fmaxf(fmaxf(mt0, x0[r]), x0[r + 1]);
+      mt1 = fmaxf(fmaxf(mt1, x1[r]), x1[r + 1]);
+    }
+    float mt = fmaxf(mt0, mt1);
+    const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+    return fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+  };
+  // the rare move of the reference maximum (after the PV products of the steps before)
+  auto rescale = [&](float mt, floatx16 &x0, floatx16 &x1) {
+    const bool move = mt > SOFTMAX_TAU;
+    if (__any(move)) {
+      const float sh = move ? mt : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        x0[r] -= sh;
+        x1[r] -= sh;
+      }
+      const float corr = fast_exp2(-sh);
+      l_part *= corr;
+      m_ref += sh;
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[c][r] *= corr;
+    }
+  };
+  // probabilities, packed as the PV operands, and their row sum
+  auto probs = [&](floatx16 &x0, floatx16 &x1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x0[r] = fast_exp2(x0[r]);
+      x1[r] = fast_exp2(x1[r]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const floatx16 &sv = t < 2 ? x0 : x1;
+      const int e0 = 8 * (t & 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pw[t][i] = pack_bf16x2(sv[e0 + 2 * i], sv[e0 + 2 * i + 1]);
+    }
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[t][i]), ones, ps, false);
+    l_part += ps;
+  };
+  // P V^T of step s (V slot s & 1); tiles past the keys skipped when `partial`
+  auto pv = [&](int s, bool partial) {
+    const uint8_t *lv = ldsv + (s & 1) * 4 * VB + hh * D * 16 + n * 16;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (partial && kend - 64 * s - 16 * t <= 0) continue;  // uniform
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[t][0], pw[t][1], pw[t][2], pw[t][3]}));
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const u32x4 w = *reinterpret_cast<const u32x4 *>(lv + t * VB + 32 * c * 16);
+        o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb, o[c], 0, 0, 0);
+      }
+    }
+  };
+  // One step of the pipeline: finish step s (its scores in c0, c1 are
+  // exponents against the reference) while scoring step s + 1 into n0, n1.
+  auto body = [&](int s, floatx16 &c0, floatx16 &c1, floatx16 &n0, floatx16 &n1) {
+    wait_vmcnt<0>();  // this wave's copies of step s's V and step s + 1's K
+    land_body(s);
+    barrier_lds();    // ... every wave's; every wave is done with step s - 1
+    issue_v(s + 1, (s + 1) & 1);
+    issue_k(s + 2, s & 1);
+    {  // an idle wave computes on zero queries and stores nothing
+      qk(s + 1, n0, n1);
+      probs(c0, c1);
+      // keeps the probabilities in this block (ahead of the mask's branch)
+      asm volatile("" ::"v"(l_part), "v"(pw[0][0]), "v"(pw[0][1]), "v"(pw[0][2]), "v"(pw[0][3]), "v"(pw[1][0]),
+                   "v"(pw[1][1]), "v"(pw[1][2]), "v"(pw[1][3]), "v"(pw[2][0]), "v"(pw[2][1]), "v"(pw[2][2]),
+                   "v"(pw[2][3]), "v"(pw[3][0]), "v"(pw[3][1]), "v"(pw[3][2]), "v"(pw[3][3]));
+      // the score products of step s + 1 interleaved with step s's probabilities
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS reads, four ahead
+#pragma unroll
+      for (int i = 0; i < 2 * D / 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if (i + 4 < 2 * D / 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      }
+      mask(s + 1, n0, n1);
+      const float mt = expo(n0, n1);
+      pv(s, false);
+      // step s's PV products interleaved with step s + 1's exponents
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // LDS reads, four ahead
+#pragma unroll
+      for (int i = 0; i < 4 * D / 32; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if (i + 4 < 4 * D / 32) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      }
+      rescale(mt, n0, n1);
+    }
+  };
 
   if (n_steps > 0) {
     issue_k(0, 0);
-    wait_vmcnt<0>();
     if constexpr (FP8) {
-      if (wave < n_tiles) convert_k(ks_next);  // uniform
-      vs_cur = vs_next;
+      wait_vmcnt<0>();
+      if (has_tile(0)) convert_k(ks_next, 0);
+    }
+    issue_v(0, 0);
+    issue_k(1, 1);
+    if constexpr (!FP8) {
+      if (has_tile(1)) wait_vmcnt<2 * NC>(); else wait_vmcnt<NC>();  // K of step 0 landed
     }
     barrier_lds();
-    for (int s = 0; s < n_steps; ++s) {
-      const int cur = s & 1;
-      issue_v(s);  // its slot was left at the last barrier
-      const bool k_next = s + 1 < n_steps && 4 * (s + 1) + wave < n_tiles;  // uniform: this wave copies K next
-      if (s + 1 < n_steps) issue_k(s + 1, cur ^ 1);
-      const int kb = 64 * s;  // position of the step's first key
-      uint32_t pw[4][4];      // PV B operands, packed bf16 probabilities
-      if (active) {
-        floatx16 s0, s1;
+    floatx16 a0, a1, b0, b1;
+    {
+      qk(0, a0, a1);
+      mask(0, a0, a1);
+      // the reference maximum starts at the first step's row maximum (every
+      // query sees key 0, so it is finite)
+      float mt = fmaxf(a0[0], a1[0]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
-        const uint8_t *lk = ldsk + ((FP8 ? 0 : cur) * 4 + (kn >> 4)) * KB + (kn & 15) * 16;
-#pragma unroll
-        for (int jj = 0; jj < D / 16; ++jj) {
-          const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + (2 * jj + hh) * 256));
-          const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(lk + 2 * KB + (2 * jj + hh) * 256));
-          s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qb[jj], s0, 0, 0, 0);
-          s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qb[jj], s1, 0, 0, 0);
-        }
-        const int min_pos = ctx + t0;  // the smallest query position of the workgroup
-        if (!(kend >= kb + 64 && kb + 63 <= min_pos)) {  // uniform: masks in this step
-          // keys of the step this lane's query sees: 0 .. lim (relative to kb and
-          // to this lane's key octet); past kend nothing is seen
-          const int pos = min_pos + n;
-          const int lim = (pos < kend - 1 ? pos : kend - 1) - kb - 8 * hh;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            if (16 * (r / 8) + (r % 8) > lim) s0[r] = -INFINITY;
-            if (32 + 16 * (r / 8) + (r % 8) > lim) s1[r] = -INFINITY;
-          }
-        }
-        if (s == 0) {  // uniform: the reference maximum starts at the first step's row maximum
-          // (every query sees key 0, so it is finite)
-          float mt = fmaxf(s0[0], s1[0]);
-#pragma unroll
-          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
-          const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-          mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1])) * scale_log2;  // the scale is positive
-          m_ref = mt == -INFINITY ? 0.f : mt;
-        }
-        // Exponents against the reference maximum; their maximum (of FMA results,
-        // which max3 takes as they are) says whether it must move.
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s0[r] = __builtin_fmaf(s0[r], scale_log2, -m_ref);  // masked: -inf
-          s1[r] = __builtin_fmaf(s1[r], scale_log2, -m_ref);
-        }
-        // two chains of max3 over the 32 exponents
-        float mt0 = fmaxf(s0[0], s0[1]), mt1 = fmaxf(s1[0], s1[1]);
-#pragma unroll
-        for (int r = 2; r < 16; r += 2) {
-          mt0 = fmaxf(fmaxf(mt0, s0[r]), s0[r + 1]);
-          mt1 = fmaxf(fmaxf(mt1, s1[r]), s1[r + 1]);
-        }
-        float mt = fmaxf(mt0, mt1);
-        {
-          const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-          mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
-        }
-        const bool move = mt > SOFTMAX_TAU;
-        if (__any(move)) {  // rare: some row's maximum rose past the reference by 2^SOFTMAX_TAU
-          const float sh = move ? mt : 0.f;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            s0[r] -= sh;
-            s1[r] -= sh;
-          }
-          const float corr = fast_exp2(-sh);
-          l_part *= corr;
-          m_ref += sh;
-#pragma unroll
-          for (int c = 0; c < D / 32; ++c)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[c][r] *= corr;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s0[r] = fast_exp2(s0[r]);  // masked: -inf -> 0
-          s1[r] = fast_exp2(s1[r]);
-        }
-        // Tile t = 2 half + st takes scores 8 st .. 8 st + 7 of its half, packed
-        // as four words. The words stay scalars until the MFMA operand is
-        // built: the dot products read them one by one (with the words as
-        // elements of a 4-vector, hipcc 7.2 fed every dot product of a vector
-        // its first element).
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const floatx16 &sv = t < 2 ? s0 : s1;
-          const int e0 = 8 * (t & 1);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) pw[t][i] = pack_bf16x2(sv[e0 + 2 * i], sv[e0 + 2 * i + 1]);
-        }
-        float ps = 0.f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[t][i]), ones, ps, false);
-        l_part += ps;
-      }
-      if (k_next)
-        wait_vmcnt<NC>();  // this step's V landed (the next step's K may be in flight)
-      else
-        wait_vmcnt<0>();
-      {
-        // The slots of a partial tile past the keys may hold NaN (0 x NaN in a
-        // PV product is NaN): the wave that copied the tile zeroes them, so
-        // the PV products read V as it stands.
-        int vt = kend - kb - 16 * wave;  // keys of this wave's tile
-        vt = vt < 0 ? 0 : (vt > 16 ? 16 : vt);
-        if (FP8 && vt > 0) {  // uniform
-          convert_v(vs_cur, vt);
-        } else if (!FP8 && vt > 0 && vt < 16) {  // uniform; at most once per workgroup
-#pragma unroll
-          for (int i = 0; i < D / 32; ++i) {
-            const int pc = 64 * i + lane;  // V piece: octet pc / D, row pc % D (8 tokens)
-            const int cnt = vt - 8 * (pc / D);  // tokens of the piece that are keys
-            u32x4 *ptr = reinterpret_cast<u32x4 *>(ldsv + wave * VB + pc * 16);
-            u32x4 w = *ptr;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              if (e >= cnt) w[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-            *ptr = w;
-          }
-        }
-      }
-      barrier_lds();  // ... for every wave
-      if (active) {
-        const uint8_t *lv = ldsv + hh * D * 16 + n * 16;  // octet hh: keys 8 hh .. 8 hh + 7 of a tile
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (kend - kb - 16 * t <= 0) continue;  // uniform: a tile past the keys (its LDS buffer is stale)
-          const bf16x8 pb = __builtin_bit_cast(bf16x8, (u32x4{pw[t][0], pw[t][1], pw[t][2], pw[t][3]}));
-#pragma unroll
-          for (int c = 0; c < D / 32; ++c) {
-            const u32x4 w = *reinterpret_cast<const u32x4 *>(lv + t * VB + 32 * c * 16);
-            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb, o[c], 0, 0, 0);
-          }
-        }
-      }
-      wait_vmcnt<0>();  // the next step's K landed
-      if constexpr (FP8) {
-        if (k_next) convert_k(ks_next);  // every wave left the K slot at the first barrier
-        vs_cur = vs_next;
-      }
-      barrier_lds();  // ... for every wave; every wave is done with this step's K and V
+      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, fmaxf(a0[r], a1[r]));
+      const auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+      mt = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1])) * scale_log2;
+      m_ref = mt == -INFINITY ? 0.f : mt;
+      rescale(expo(a0, a1), a0, a1);
+    }
+    // the last step: its V, its probabilities, its PV products (tiles past the keys skipped)
+    auto tail = [&](int s, floatx16 &c0, floatx16 &c1) {
+      wait_vmcnt<0>();
+      land(s);
+      barrier_lds();
+      probs(c0, c1);
+      pv(s, true);
+    };
+    const int n_body = n_steps - 1;
+    int s = 0;
+    for (; s + 2 <= n_body; s += 2) {
+      body(s, a0, a1, b0, b1);
+      body(s + 1, b0, b1, a0, a1);
+    }
+    if (s < n_body) {
+      body(s, a0, a1, b0, b1);
+      tail(s + 1, b0, b1);
+    } else {
+      tail(s, a0, a1);
     }
   }
   const int tok = t0 + n;
