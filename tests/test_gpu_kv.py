@@ -94,6 +94,39 @@ def test_append_bf16_many_tokens_shuffled_slots_bit_exact(cuda, H, D, BS, T):
     _assert_cache_equal(cache, kc, vc, what=f"bulk append T={T}")
 
 
+@pytest.mark.parametrize("H,D,BS", [(8, 128, 16), (2, 64, 32), (3, 128, 64)])
+def test_append_bf16_prompt_runs_bit_exact(cuda, H, D, BS):
+    """Prompt-shaped appends through the transposing kernel: each sequence's tokens at
+    consecutive positions of its blocks (a random block order), continuing cached contexts of
+    0, 8, 3, 13, 21 tokens (8-token groups that start aligned, mid-group and mid-block), one
+    skipped token (-1) and a ragged end: the 16-byte V stores of aligned groups and the
+    per-token stores of the others, bit-exact against the oracle."""
+    rng = np.random.default_rng(BS * 7 + D)
+    ctx = [0, 8, 3, 13, 21]
+    new = [300, 77, 129, 64, 250]
+    per_seq = [-(-(c + n) // BS) for c, n in zip(ctx, new)]
+    NB = sum(per_seq) + 4
+    order = rng.permutation(NB)
+    slots, used = [], 0
+    for c, n, nb in zip(ctx, new, per_seq):
+        blocks = order[used:used + nb]
+        used += nb
+        pos = np.arange(c, c + n)
+        slots.append(blocks[pos // BS].astype(np.int64) * BS + pos % BS)
+    slots = np.concatenate(slots)
+    slots[101] = -1
+    T = len(slots)
+    assert T >= 256  # the transposing kernel's range
+    kc, vc = paged.empty_cache(NB, BS, H, D, fill=0xFFFF)
+    cache = PagedKVCache(NB, BS, H, D, device=cuda)
+    _upload(cache, kc, vc)
+    kv = synth.normal_bf16(synth.stream_key("prompt-runs", str(BS), str(D)), (T, 2 * H, D))
+    paged.append_bf16(kc, vc, kv[:, :H], kv[:, H:], slots)
+    d = to_dev_bits(kv, BF16, cuda)
+    cache.append(d[:, :H], d[:, H:], torch.from_numpy(slots).to(cuda))
+    _assert_cache_equal(cache, kc, vc, what=f"prompt runs BS={BS} D={D}")
+
+
 def _exhaustive_bf16_rows(h: int, d: int) -> np.ndarray:
     """All 65,536 bf16 patterns sorted by magnitude (NaN last), as [tokens, h, d]."""
     bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)

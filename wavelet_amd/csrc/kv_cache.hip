@@ -41,12 +41,18 @@ __global__ __launch_bounds__(256) void append_bf16_kernel(uint16_t *__restrict__
 }
 
 // bf16 append of many tokens (a prompt): workgroup = 64 consecutive tokens x
-// one head. Rows are read whole (16 bytes per thread, coalesced) into LDS,
-// transposed, and written with lanes along tokens: thread i always owns token
-// i % 64 (its slot loaded once), so one K store instruction writes 64 tokens'
-// 16-byte pieces of one chunk and one V store 64 tokens' values of one d row --
-// contiguous runs of the cache's [.., BS, 8] / [.., D, BS] rows wherever the
-// slots are consecutive, instead of 2-byte writes to 64 different rows.
+// one head, rows read whole (16 bytes per thread, coalesced). K ([.., C, BS,
+// 8]: a chunk's pieces of a block's tokens are contiguous) is stored from the
+// registers as loaded: 16-byte pieces, 64-byte runs per store instruction
+// where the slots are consecutive. V ([.., D, BS]: a row of the cache holds
+// one d of a block's tokens) goes through LDS: the window's tokens go in
+// groups of 8; a group whose 8 slots are consecutive and start 8-aligned in
+// one block (every group of a prompt that starts on an 8-token boundary) is
+// written as one 16-byte piece per d row, lanes along (d, group pair) so that
+// a store instruction covers 32 whole 32-byte rows of a 16-token block; other
+// groups (scattered slots, skipped tokens, a sequence starting mid-group, the
+// ragged end) fall back to 2-byte stores per token. 17 KB of LDS at d=128:
+// the whole prompt's workgroups are resident at once.
 constexpr int kBulkTokens = 64;
 constexpr int64_t kBulkMinTokens = 256;  // below this (a decode step's tokens) the per-chunk kernel spreads wider
 
@@ -58,10 +64,10 @@ __global__ __launch_bounds__(256) void append_bf16_bulk_kernel(uint16_t *__restr
                                                                const int64_t *__restrict__ slots, int64_t T, int H,
                                                                int BS, int64_t NB) {
   constexpr int C = D / 8;
-  constexpr int KP = kBulkTokens + 1;      // K pitch in 16-byte pieces: chunk rows land 4 banks apart
-  constexpr int VP = kBulkTokens * 2 + 4;  // V pitch in bytes (2-way conflicts at most on the transposing write)
-  __shared__ __attribute__((aligned(16))) u32x4 lk[C * KP];
-  __shared__ __attribute__((aligned(16))) uint8_t lv[D * VP];
+  constexpr int RP = D * 2 + 8;        // V pitch in bytes per token row: rows 8 apart land 16 banks apart
+  constexpr int NG = kBulkTokens / 8;  // token groups of the window
+  __shared__ __attribute__((aligned(16))) uint8_t lv[kBulkTokens * RP];
+  __shared__ int64_t gslot[NG];  // a group's first slot when its 8 slots are one aligned run, else -1
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kBulkTokens;
   const int h = blockIdx.y;
   const int tid = threadIdx.x;
@@ -74,29 +80,60 @@ __global__ __launch_bounds__(256) void append_bf16_bulk_kernel(uint16_t *__restr
       if (t0 + t < T) {
         const u32x4 kv = *reinterpret_cast<const u32x4 *>(key + (t0 + t) * kst + h * ksh + c * 8);
         const u32x4 vv = *reinterpret_cast<const u32x4 *>(val + (t0 + t) * vst + h * vsh + c * 8);
-        lk[c * KP + t] = kv;
+        const int64_t slot = slots[t0 + t];
+        const int64_t blk = slot / BS;
+        if (slot >= 0 && blk < NB)
+          *reinterpret_cast<u32x4 *>(kc + (((blk * H + h) * C + c) * BS + slot % BS) * 8) = kv;
+        uint32_t *w = reinterpret_cast<uint32_t *>(&lv[t * RP + c * 16]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<uint16_t *>(&lv[(c * 8 + j) * VP + t * 2]) =
-              static_cast<uint16_t>(vv[j >> 1] >> (16 * (j & 1)));
+        for (int j = 0; j < 4; ++j) w[j] = vv[j];
       }
+    }
+    if (tid < NG) {
+      const int64_t ta = t0 + 8 * tid;
+      int64_t first = -1;
+      if (ta + 7 < T && BS % 8 == 0) {
+        first = slots[ta];
+        const bool start = first >= 0 && first / BS < NB && (first % BS) % 8 == 0;
+        bool run = start;
+#pragma unroll
+        for (int j = 1; j < 8; ++j) run = run && slots[ta + j] == first + j;
+        if (!run) first = -1;
+      }
+      gslot[tid] = first;
     }
   }
   __syncthreads();
-  const int t = tid % kBulkTokens;
-  if (t0 + t >= T) return;
-  const int64_t slot = slots[t0 + t];
-  if (slot < 0) return;
-  const int64_t blk = slot / BS;
-  const int off = static_cast<int>(slot % BS);
-  if (blk >= NB) return;  // out-of-range ids are never written (no fault)
-  const int r0 = tid / kBulkTokens;  // 0..3
-  uint16_t *kdst = kc + ((blk * H + h) * C * BS + off) * 8;
+  // V: item i -> group pair gp = i / (2 D), d = (i / 2) % D, group 2 gp + i % 2
 #pragma unroll
-  for (int c = r0; c < C; c += 4) *reinterpret_cast<u32x4 *>(kdst + static_cast<int64_t>(c) * BS * 8) = lk[c * KP + t];
-  uint16_t *vdst = vc + (blk * H + h) * D * BS + off;
-#pragma unroll 8
-  for (int d = r0; d < D; d += 4) vdst[static_cast<int64_t>(d) * BS] = *reinterpret_cast<const uint16_t *>(&lv[d * VP + t * 2]);
+  for (int k = 0; k < NG * D / 256; ++k) {
+    const int i = tid + 256 * k;
+    const int g = 2 * (i / (2 * D)) + (i & 1);
+    const int d = (i >> 1) % D;
+    const int64_t first = gslot[g];
+    if (first >= 0) {  // one aligned run: 8 tokens of row d in one 16-byte piece
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = *reinterpret_cast<const uint16_t *>(&lv[(8 * g + 2 * j) * RP + 2 * d]);
+        const uint32_t hi = *reinterpret_cast<const uint16_t *>(&lv[(8 * g + 2 * j + 1) * RP + 2 * d]);
+        w[j] = lo | (hi << 16);
+      }
+      const int64_t blk = first / BS;
+      const int off = static_cast<int>(first % BS);
+      *reinterpret_cast<u32x4 *>(vc + ((blk * H + h) * D + d) * BS + off) = u32x4{w[0], w[1], w[2], w[3]};
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = 8 * g + j;
+        if (t0 + t >= T) break;
+        const int64_t slot = slots[t0 + t];
+        const int64_t blk = slot / BS;
+        if (slot < 0 || blk >= NB) continue;
+        vc[((blk * H + h) * D + d) * BS + slot % BS] = *reinterpret_cast<const uint16_t *>(&lv[t * RP + 2 * d]);
+      }
+    }
+  }
 }
 
 template <int D>
