@@ -260,7 +260,8 @@ def test_fused_mla_append_decode_equals_append_then_decode(cuda, heads, bs, part
 
 @pytest.mark.parametrize("shared", [False, True])
 @pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
-@pytest.mark.parametrize("hq,hkv,d,bs", [(32, 8, 128, 16), (14, 2, 64, 16), (16, 4, 128, 64)])
+@pytest.mark.parametrize("hq,hkv,d,bs", [(32, 8, 128, 16), (14, 2, 64, 16), (16, 4, 128, 64), (32, 8, 128, 32),
+                                         (14, 2, 64, 128), (8, 2, 128, 256)])
 def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, d, bs, shared):
     """One launch (append + attention) leaves the cache bit-identical to wkv_append(_fp8) and
     attends within tolerance (bf16 attends the new token from its inputs, a different summation
