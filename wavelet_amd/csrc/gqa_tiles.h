@@ -227,11 +227,20 @@ __device__ __forceinline__ void attend_tile(DecodeState<D, FP8> &st, const Tile<
 #pragma unroll
       for (int e = 0; e < 4; ++e) v8[4 * j + e] = w[e];
     }
+    if (t.valid < 16) {
+      // Never let a masked slot's V reach the accumulator (it may hold NaN):
+      // code 0 is +0, widened to the bf16 zero. Byte e of every dword is
+      // token 4 grp + e; one mask for all of them.
+      const int keep = t.valid - 4 * grp;
+      const uint32_t m = keep >= 4 ? 0xffffffffu : (keep <= 0 ? 0u : (1u << (8 * keep)) - 1u);
+#pragma unroll
+      for (int n = 0; n < D / 16; ++n) v8[n] &= m;
+    }
   }
 #pragma unroll
   for (int n = 0; n < D / 16; ++n) {
     shortx4 vop = FP8 ? fp8x4_to_bf16x4(v8[FP8 ? n : 0]) : __builtin_bit_cast(shortx4, t.v[FP8 ? 0 : n]);
-    if (t.valid < 16) {
+    if (!FP8 && t.valid < 16) {
       // Never let a masked slot's V reach the accumulator (it may hold NaN).
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -316,10 +325,22 @@ __device__ __forceinline__ void attend_range(Consume &&consume, const uint8_t *_
   // block) is issued with a zero-record resource: no memory is read for it
   // (re-reading the last tile instead cost 4% more HBM reads once the tiles
   // were loaded non-temporally, as the re-read no longer hit the L2).
+  // Tile i's first token, its block (relative to blk_first) and its offset in
+  // that block, kept as counters: issue() is called for i = 0, 1, 2, ... in
+  // order, and a tile past the end keeps the last tile's position (its loads
+  // read nothing). A division by the runtime block size per tile cost about
+  // 20 scalar instructions.
+  int c_ts = t_begin, c_bi = 0, c_off = t_begin - blk_first * BS;
   auto issue = [&](Tile<D, FP8> &t, int i) {
-    const int ii = i < n_tiles ? i : n_tiles - 1;
-    const int ts = t_begin + 16 * ii;
-    const int bi = ts / BS - blk_first;
+    const int ts = c_ts, bi = c_bi, o0 = c_off;
+    if (i + 1 < n_tiles) {  // uniform: 16 tokens on, at most one block boundary (BS is a multiple of 16)
+      c_ts += 16;
+      c_off += 16;
+      if (c_off >= BS) {
+        c_off -= BS;
+        ++c_bi;
+      }
+    }
     int blk = __builtin_amdgcn_readlane(my_blk, bi);
     const bool live = i < n_tiles && blk >= 0;
     t.valid = live ? ((t_end - ts) < 16 ? (t_end - ts) : 16) : 0;
@@ -332,7 +353,7 @@ __device__ __forceinline__ void attend_range(Consume &&consume, const uint8_t *_
       t.vsc = 1.f;
     }
     if (blk < 0) blk = 0;
-    load_tile<D, FP8>(t, kc, vc, blk, kvh, Hkv, BS, ts % BS, koff, voff, stream, live);
+    load_tile<D, FP8>(t, kc, vc, blk, kvh, Hkv, BS, o0, koff, voff, stream, live);
   };
   // Loads are issued unconditionally, which keeps the wait counts exact; a
   // tile past the end (or of an unmapped block) is skipped, uniformly, when its
