@@ -205,7 +205,7 @@ def test_decode_mla_batches_of_eight(cuda, heads, partition):
               tag=f"b16h{heads}p{partition}")
 
 
-@pytest.mark.parametrize("bs,partition", [(16, 32), (16, 0), (64, 96), (32, 160), (128, 32)])
+@pytest.mark.parametrize("bs,partition", [(16, 32), (16, 0), (64, 96), (32, 160), (128, 32), (256, 96), (256, 0)])
 def test_decode_mla_block_sizes_and_partitions(cuda, bs, partition):
     """32-token steps that straddle two blocks, partitions that start inside a block,
     and tails that end inside a step (NaN in every slot no sequence owns)."""
@@ -214,7 +214,8 @@ def test_decode_mla_block_sizes_and_partitions(cuda, bs, partition):
 
 
 @pytest.mark.parametrize("heads,bs,partition,nseq",
-                         [(128, 64, 0, 10), (16, 64, 96, 10), (64, 16, 32, 10), (32, 32, 0, 10), (128, 64, 64, 16)])
+                         [(128, 64, 0, 10), (16, 64, 96, 10), (64, 16, 32, 10), (32, 32, 0, 10), (128, 64, 64, 16),
+                          (128, 256, 0, 16), (32, 128, 160, 10)])
 def test_fused_mla_append_decode_equals_append_then_decode(cuda, heads, bs, partition, nseq):
     """One launch (latent append + MLA attention) leaves the cache bit-identical to
     wkv_mla_append and attends within tolerance of the separate path and of the oracle; the new
