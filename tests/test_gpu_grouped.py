@@ -95,6 +95,8 @@ CASES = [
     (32, 8, 128, 16, 2, 3, (257, 512), 33),         # 24 rows
     (16, 1, 128, 64, 1, 16, (700,), 20),            # 256 rows per group: 16 row tiles, 4 workgroups
     (8, 8, 64, 16, 5, 1, (40, 64, 1, 200, 90), 9),  # groups of one
+    (28, 4, 128, 32, 2, 8, (1024, 500), 100),       # block 32, a prompt ending mid-block
+    (16, 2, 128, 128, 2, 4, (600, 129), 50),        # block 128
 ]
 
 
