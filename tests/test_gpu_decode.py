@@ -94,7 +94,9 @@ def test_decode_qwen3_4b_shape_variable_lengths(cuda):
         _gqa_case(w, cuda, partition_size=p)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (28, 4, 128), (16, 1, 128), (8, 8, 64)])
+# Qwen3-4B, Qwen2.5-0.5B, Qwen2.5-7B, 16 heads on one KV head, GPT-OSS-like, Qwen3-30B-A3B, Qwen3-0.6B
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (28, 4, 128), (16, 1, 128), (8, 8, 64), (32, 4, 128),
+                                     (16, 8, 128)])
 def test_decode_edge_lengths_and_partitions(cuda, hq, hkv, d):
     lens = np.array([0, 1, 2, 15, 16, 17, 63, 255, 256, 257, 700, 1024])
     w = synth.make_decode_workload(f"edge{hq}x{hkv}x{d}", batch=len(lens), num_kv_heads=hkv, num_q_heads=hq,
@@ -262,7 +264,7 @@ def test_fused_mla_append_decode_equals_append_then_decode(cuda, heads, bs, part
 @pytest.mark.parametrize("shared", [False, True])
 @pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("hq,hkv,d,bs", [(32, 8, 128, 16), (14, 2, 64, 16), (16, 4, 128, 64), (32, 8, 128, 32),
-                                         (14, 2, 64, 128), (8, 2, 128, 256)])
+                                         (14, 2, 64, 128), (8, 2, 128, 256), (32, 4, 128, 16), (16, 8, 128, 16)])
 def test_fused_append_decode_equals_append_then_decode(cuda, kv_dtype, hq, hkv, d, bs, shared):
     """One launch (append + attention) leaves the cache bit-identical to wkv_append(_fp8) and
     attends within tolerance (bf16 attends the new token from its inputs, a different summation
