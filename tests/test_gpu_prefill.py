@@ -99,7 +99,7 @@ MIX = ([37, 16, 1, 130, 0, 64, 200], [37, 300, 50, 1000, 20, 64, 900])
 
 @pytest.mark.parametrize("kv_dtype", ["bf16", "fp8_e4m3"])
 @pytest.mark.parametrize("hq,hkv,d,bs", [(32, 8, 128, 16), (14, 2, 64, 16), (28, 4, 128, 16), (16, 16, 128, 64),
-                                         (8, 1, 64, 32), (16, 4, 128, 128), (8, 2, 64, 256)])
+                                         (8, 1, 64, 32), (16, 4, 128, 128), (8, 2, 64, 256), (16, 8, 128, 16)])
 def test_prefill_varlen_chunked(cuda, kv_dtype, hq, hkv, d, bs):
     name = f"pf{kv_dtype}{hq}{hkv}{d}{bs}"
     w, cache, host, new = _case(cuda, name, hq, hkv, d, bs, *MIX, kv_dtype)
