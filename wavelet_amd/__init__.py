@@ -18,6 +18,12 @@ Public surface (a drop-in for the KV path of the reference's inference engine):
   sleep / wake_up lifecycle and KV metrics;
 * ``sample`` -- the token sampler after decode (temperature, min_p, top_k,
   top_p, repetition penalty; processed logprobs and the sampling mask).
+
+Also, by module: ``wavelet_amd.plan`` -- a whole decode or prompt step over
+every layer, built once and launched per step (``DecodeStep``,
+``MLADecodeStep``, ``PrefillStep``), and ``GraphDecodeStep``, the decode step
+captured in one HIP graph; ``wavelet_amd.hf`` -- a transformers ``Cache`` over
+a ``KVPool`` and the ``"wavelet_paged"`` attention implementation.
 """
 
 from .attention import (decode_order, decode_plan, grouped_decode_order, paged_decode_gqa, paged_decode_gqa_grouped,
